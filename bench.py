@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused causal attention path (fwd + bwd) on one MI355X.
+
+Metric: causal attention fwd+bwd TFLOP/s and % of the fp32
+MFMA peak at B=8 T=1024 H=12 D=64 (config C2).  One "step" = one forward
+(attention_forward_cuda_kernel) + one backward
+(attention_backward_cuda_kernel) over the same synthetic batch, through the
+library's C-ABI, inputs and outputs resident in HBM, nothing allocated in
+the timed region.
+
+FLOPs are algorithmic: the two forward and four backward contractions over
+the causal triangle only, D*T*(T+1)*B*H flop each (T(T+1)/2 query-key pairs
+x D multiply-adds x 2), no recompute, no softmax.  fwd = 2 units, bwd = 4.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import ctypes
+import json
+import os
+import re
+import statistics
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gpt.c_amd"))
+
+import numpy as np  # noqa: E402
+
+import gptc  # noqa: E402
+
+METRIC = "causal attn fwd+bwd TFLOP/s + % fp32 MFMA peak, B=8 T=1024 H=12 D=64"
+CONFIGS = {
+    "c2": dict(B=8, T=1024, C=768, H=12, workload="causal self-attention fwd+bwd, GPT-2 124M shape (C2)"),
+    "c5": dict(B=4, T=1024, C=1600, H=25, workload="causal self-attention fwd+bwd, GPT-2 XL shape (C5)"),
+    "c1": dict(B=8, T=128, C=768, H=12, workload="causal self-attention fwd+bwd at C1's shape"),
+}
+SEED_X, SEED_DY = 1337, 1338
+SPEC_CU, SPEC_MHZ = 256, 2400            # MI355X public spec
+FLOP_PER_CLK_CU_FP32_MFMA = 256          # v_mfma_f32_32x32x2_f32: 4096 flop / 16 passes of 4 clk, 4 SIMDs
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def device_peak():
+    """fp32 MFMA peak from rocminfo's CU count and max clock (spec fallback)."""
+    cu, mhz, src = SPEC_CU, SPEC_MHZ, "spec"
+    try:
+        out = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
+        for block in out.split("Agent ")[1:]:
+            if "gfx950" not in block:
+                continue
+            m_cu = re.search(r"Compute Unit:\s+(\d+)", block)
+            m_mhz = re.search(r"Max Clock Freq\. \(MHz\):\s+(\d+)", block)
+            if m_cu and m_mhz:
+                cu, mhz, src = int(m_cu.group(1)), int(m_mhz.group(1)), "rocminfo"
+            break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return cu * mhz * 1e6 * FLOP_PER_CLK_CU_FP32_MFMA / 1e12, cu, mhz, src
+
+
+class Hip:
+    """The few HIP runtime calls the timer needs (ctypes on libamdhip64)."""
+
+    def __init__(self):
+        self.h = ctypes.CDLL("libamdhip64.so")
+        self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError {rc}")
+
+    def event(self):
+        e = ctypes.c_void_p()
+        self.check(self.h.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, ev, stream):
+        self.check(self.h.hipEventRecord(ev, stream), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self.check(self.h.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self.check(self.h.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+    def device_sync(self):
+        self.check(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+def contraction_flops(B, T, H, D):
+    return float(D) * T * (T + 1) * B * H
+
+
+def cpu_baseline(cfg, x, dy, budget_s):
+    """The oracle (C restatement of gpt.c's OpenBLAS CPU path) on this host."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as oracle_mod
+    threads = min(16, os.cpu_count() or 1)
+    orc = oracle_mod.Oracle(threads=threads)
+    B, T, C, H = cfg["B"], cfg["T"], cfg["C"], cfg["H"]
+    times = []
+    t_start = time.perf_counter()
+    for i in range(4):
+        t0 = time.perf_counter()
+        _, q, k, v, att = orc.forward(x, H)
+        t1 = time.perf_counter()
+        orc.backward(dy, H, q, k, v, att)
+        t2 = time.perf_counter()
+        if i > 0:
+            times.append((t1 - t0, t2 - t1))
+        log(f"[cpu] run {i}: fwd {t1 - t0:.3f} s bwd {t2 - t1:.3f} s")
+        if time.perf_counter() - t_start > budget_s and len(times) >= 1:
+            break
+    fwd = statistics.median(t[0] for t in times)
+    bwd = statistics.median(t[1] for t in times)
+    flops = 6 * contraction_flops(B, T, H, C // H)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            m = re.search(r"model name\s*:\s*(.*)", f.read())
+            model = m.group(1).strip() if m else ""
+    except OSError:
+        pass
+    return {
+        "value": flops / (fwd + bwd) / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"one full {cfg['workload']} step (B={B} T={T} H={H}), 1 warm-up then median of "
+                   f"{len(times)}; fwd {fwd * 1e3:.1f} ms + bwd {bwd * 1e3:.1f} ms; OPENBLAS threads={threads}; "
+                   f"{orc.blas_config}; host '{model}', nproc={os.cpu_count()}"),
+        "ms_per_step": (fwd + bwd) * 1e3,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget-s", type=float, default=20.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (every (b, h) pair of causal attention is "
+              "independent; see DESIGN.md for how the path shards). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    cfg = CONFIGS[args.config]
+    B, T, C, H = cfg["B"], cfg["T"], cfg["C"], cfg["H"]
+    D = C // H
+    lib = gptc.load()
+    rt = gptc.Runtime(lib)
+    rt.init()
+    hip = Hip()
+    stream = rt.stream()
+
+    x = rt.normal((B, T, 3 * C), SEED_X)
+    dy = rt.normal((B, T, C), SEED_DY)
+    xt = rt.from_numpy(x)
+    dyt = rt.from_numpy(dy)
+    mask = rt.from_numpy(np.tril(np.ones((T, T), np.float32)))
+    # Compact cache layout of the library's Attention(): cache[0] is the input itself.
+    caches = (gptc.TensorP * 4)(xt, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((B, H, T)))
+    yt = rt.empty((B, T, C))
+    dqkv = rt.empty((B, T, 3 * C))
+    rt.sync()
+
+    def step():
+        lib.attention_forward_cuda_kernel(xt, mask, H, caches, yt)
+        lib.attention_backward_cuda_kernel(dyt, caches, H, dqkv)
+
+    log(f"[bench] {cfg['workload']}: B={B} T={T} H={H} D={D}; warmup {args.warmup}, steps {args.steps}")
+    for _ in range(args.warmup):
+        step()
+    rt.sync()
+    hip.device_sync()
+
+    evs = [[hip.event() for _ in range(6)] for _ in range(args.steps)]
+    ev_arrays = [(ctypes.c_void_p * 6)(*e) for e in evs]
+    t_begin, t_end = hip.event(), hip.event()
+    hip.record(t_begin, stream)
+    for i in range(args.steps):
+        lib.gptc_set_kernel_events(ev_arrays[i], 6)
+        step()
+    hip.record(t_end, stream)
+    rt.sync()
+    hip.device_sync()
+    lib.gptc_set_kernel_events(None, 0)
+    total_ms = hip.elapsed_ms(t_begin, t_end)
+    k_ms = {name: statistics.mean(hip.elapsed_ms(e[2 * j], e[2 * j + 1]) for e in evs)
+            for j, name in enumerate(("fwd", "bwd_dq", "bwd_dkdv"))}
+    ms_per_step = total_ms / args.steps
+
+    unit = contraction_flops(B, T, H, D)
+    flops = 6 * unit
+    peak, cu, mhz, peak_src = device_peak()
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    kernel_flops = {"fwd": 2 * unit, "bwd_dq": 1 * unit, "bwd_dkdv": 3 * unit}
+    dom = max(k_ms, key=k_ms.get)
+    achieved = kernel_flops[dom] / (k_ms[dom] * 1e-3) / 1e12
+    log(f"[bench] {ms_per_step:.4f} ms/step, {value:.2f} TFLOP/s; kernels (ms): " +
+        ", ".join(f"{k} {v:.4f}" for k, v in k_ms.items()))
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": f"synthetic: qkv ~ N(0,1) seed {SEED_X}, dout ~ N(0,1) seed {SEED_DY} (torch-identical mt19937)",
+        "config": {"workload": cfg["workload"], "B": B, "T": T, "H": H, "D": D, "C": C,
+                   "causal_flop_per_step": flops},
+        "pct_fp32_mfma_peak": round(100.0 * value / peak, 2),
+        "tokens_per_s": round(B * T / (ms_per_step * 1e-3), 1),
+        "peak_tflops": round(peak, 2),
+        "peak_source": f"{peak_src}: {cu} CU x {mhz} MHz x {FLOP_PER_CLK_CU_FP32_MFMA} flop/clk/CU",
+        "kernel_ms": {k: round(v, 5) for k, v in k_ms.items()},
+        "roofline": {
+            "kernel": dom,
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": round(peak, 2),
+            "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+            "algorithmic_flop_per_launch": kernel_flops[dom],
+        },
+    }
+    for t in (dyt, mask, yt, dqkv, *caches):
+        rt.free(t)
+    rt.sync()
+
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle over OpenBLAS) ...")
+        cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s)
+        result["cpu_baseline"] = {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cb.items()}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

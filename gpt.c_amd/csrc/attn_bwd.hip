@@ -1,0 +1,334 @@
+// Fused causal attention backward for gfx950 (FlashAttention-2 style:
+// P is rebuilt from the saved log-sum-exp, never stored).  Replaces
+// gpt.c's unpermute / 4 batched SGEMMs / softmax backward / permute
+// sequence (kernels/src/cuda/Attention.cu:235-324; math of
+// kernels/src/cpu/Attention.c:169-301):
+//     dP = dO V^T,  dV = P^T dO,  dS = P o (dP - rowsum(dP o P)),
+//     dQ = dS K / sqrt(D),  dK = dS^T Q / sqrt(D),
+// using rowsum(dP o P) = rowsum(dO o O) =: delta.
+//
+// Two kernels, each writing its outputs exactly once (no atomics, no
+// zeroed output needed, deterministic):
+//   attn_bwd_dq_kernel    query-parallel (like the forward): per 32-query
+//                         wave, S^T, dP^T, dS^T over the key tiles and
+//                         dQ^T += K^T dS^T.  Also computes delta from dO
+//                         and O and stores it for the second kernel.
+//   attn_bwd_dkdv_kernel  key-parallel: per 32-key wave (K, V resident in
+//                         registers), S, dP, dS over the query tiles and
+//                         dV += P^T dO, dK += dS^T Q.
+// In both, the accumulator of the score product is directly the operand
+// of the gradient products (see the layout note in attn_common.hpp).
+#include "attn_common.hpp"
+#include "attn_kernels.hpp"
+#include "hip_check.hpp"
+
+namespace gptc {
+
+constexpr int kBwdBM = 128;  // queries per dq workgroup (32 per wave)
+constexpr int kBwdBN = 64;   // keys per LDS tile in the dq kernel
+constexpr int kBwdBK = 128;  // keys per dk/dv workgroup (32 per wave)
+constexpr int kBwdBQ = 64;   // queries per LDS tile in the dk/dv kernel
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
+    __shared__ __attribute__((aligned(16))) float k_lds[kBwdBN * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float v_lds[kBwdBN * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
+    const int bh = blockIdx.x % a.bh_pad;
+    if (bh >= a.B * a.H) return;
+    const int qb = a.nqb - 1 - static_cast<int>(blockIdx.x / a.bh_pad);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int T = a.T, D = a.D;
+
+    const int q_blk0 = qb * kBwdBM;
+    const int qw0 = q_blk0 + 32 * w;
+    const int my_q = qw0 + l32;
+    const bool q_ok = my_q < T;
+
+    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
+    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
+    const float *Orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh;
+    const float *dOrow = a.dout.p + b * a.dout.sb + my_q * a.dout.st + h * a.dout.sh;
+
+    f32x4 qr[8], dr[8];
+    float dsum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int dim = 8 * j + 4 * hf;
+        qr[j] = q_ok ? load4<VEC>(Qh + my_q * a.q.st, dim, D) : zero4();
+        dr[j] = q_ok ? load4<VEC>(dOrow, dim, D) : zero4();
+        const f32x4 orj = q_ok ? load4<VEC>(Orow, dim, D) : zero4();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dsum = fmaf(dr[j][c], orj[c], dsum);
+    }
+    const float delta = dsum + other_half(dsum);
+    const uint32_t stat = static_cast<uint32_t>(bh) * T + my_q;
+    if (q_ok && hf == 0) a.delta[stat] = delta;
+    const float lse2 = q_ok ? a.lse[stat] * kLog2e : 0.0f;
+
+    const int kv_end = min(T, q_blk0 + kBwdBM);
+    const int n_tiles = (kv_end + kBwdBN - 1) / kBwdBN;
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    f32x4 kpre[4], vpre[4];
+    auto prefetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = kt * kBwdBN + ld_row + 16 * i;
+            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
+            vpre[i] = (key < T) ? load4<VEC>(Vh + key * a.v.st, ld_col, D) : zero4();
+        }
+    };
+    prefetch(0);
+
+    const float c2 = a.scale_log2;
+    f32x16 acc_dq[2] = {zero16(), zero16()};
+
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ld_row + 16 * i;
+            *reinterpret_cast<f32x4 *>(&k_lds[row * kLdsStride + ld_col]) = kpre[i];
+            *reinterpret_cast<f32x4 *>(&v_lds[row * kLdsStride + ld_col]) = vpre[i];
+        }
+        __syncthreads();
+        if (kt + 1 < n_tiles) prefetch(kt + 1);
+
+        const int k0 = kt * kBwdBN;
+        if (k0 > qw0 + 31 || qw0 >= T) continue;
+
+        f32x16 s[2] = {zero16(), zero16()};
+        f32x16 dp[2] = {zero16(), zero16()};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int col = 8 * j + 4 * hf;
+            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&k_lds[l32 * kLdsStride + col]);
+            const f32x4 kb = *reinterpret_cast<const f32x4 *>(&k_lds[(32 + l32) * kLdsStride + col]);
+            const f32x4 va = *reinterpret_cast<const f32x4 *>(&v_lds[l32 * kLdsStride + col]);
+            const f32x4 vb = *reinterpret_cast<const f32x4 *>(&v_lds[(32 + l32) * kLdsStride + col]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s[0] = mfma32(ka[c], qr[j][c], s[0]);
+                s[1] = mfma32(kb[c], qr[j][c], s[1]);
+                dp[0] = mfma32(va[c], dr[j][c], dp[0]);
+                dp[1] = mfma32(vb[c], dr[j][c], dp[1]);
+            }
+        }
+
+        const bool diag = k0 + kBwdBN - 1 > qw0;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float p = fast_exp2(fmaf(s[kb][r], c2, -lse2));
+                if (diag) {
+                    const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (key > my_q) p = 0.0f;
+                }
+                s[kb][r] = p * (dp[kb][r] - delta);  // dS^T
+            }
+
+        // dQ^T (dims x queries) += K^T dS^T
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int row = 32 * kb + 8 * g + 4 * hf + c;
+                    const float ka0 = k_lds[row * kLdsStride + l32];
+                    const float ka1 = k_lds[row * kLdsStride + 32 + l32];
+                    acc_dq[0] = mfma32(ka0, s[kb][4 * g + c], acc_dq[0]);
+                    acc_dq[1] = mfma32(ka1, s[kb][4 * g + c], acc_dq[1]);
+                }
+    }
+
+    if (!q_ok) return;
+    float *dqrow = a.dq.p + b * a.dq.sb + my_q * a.dq.st + h * a.dq.sh;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 val;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) val[c] = acc_dq[db][4 * g + c] * a.scale;
+            store4<VEC>(dqrow, 32 * db + 8 * g + 4 * hf, D, val);
+        }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
+    __shared__ __attribute__((aligned(16))) float q_lds[kBwdBQ * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float do_lds[kBwdBQ * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float lse_lds[kBwdBQ];
+    __shared__ __attribute__((aligned(16))) float dl_lds[kBwdBQ];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
+    const int bh = blockIdx.x % a.bh_pad;
+    if (bh >= a.B * a.H) return;
+    // Low key blocks see the most queries: launch them first.
+    const int kb_idx = static_cast<int>(blockIdx.x / a.bh_pad);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int T = a.T, D = a.D;
+
+    const int k_blk0 = kb_idx * kBwdBK;
+    const int kw0 = k_blk0 + 32 * w;
+    const int my_k = kw0 + l32;
+    const bool k_ok = my_k < T;
+
+    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
+    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
+    const float *dOh = a.dout.p + b * a.dout.sb + h * a.dout.sh;
+    const float *lse_h = a.lse + static_cast<uint32_t>(bh) * T;
+    const float *dl_h = a.delta + static_cast<uint32_t>(bh) * T;
+
+    f32x4 kr[8], vr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int dim = 8 * j + 4 * hf;
+        kr[j] = k_ok ? load4<VEC>(Kh + my_k * a.k.st, dim, D) : zero4();
+        vr[j] = k_ok ? load4<VEC>(Vh + my_k * a.v.st, dim, D) : zero4();
+    }
+
+    const int qt0 = k_blk0 / kBwdBQ;
+    const int n_qt = (T + kBwdBQ - 1) / kBwdBQ;
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    f32x4 qpre[4], dpre[4];
+    float stat_pre = 0.0f;
+    auto prefetch = [&](int qt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = qt * kBwdBQ + ld_row + 16 * i;
+            qpre[i] = (q < T) ? load4<VEC>(Qh + q * a.q.st, ld_col, D) : zero4();
+            dpre[i] = (q < T) ? load4<VEC>(dOh + q * a.dout.st, ld_col, D) : zero4();
+        }
+        if (tid < 2 * kBwdBQ) {
+            const int q = qt * kBwdBQ + (tid & (kBwdBQ - 1));
+            // Rows past T get lse = +inf (P = 0) and delta = 0.
+            if (tid < kBwdBQ) stat_pre = (q < T) ? lse_h[q] * kLog2e : INFINITY;
+            else stat_pre = (q < T) ? dl_h[q] : 0.0f;
+        }
+    };
+    if (qt0 < n_qt) prefetch(qt0);
+
+    const float c2 = a.scale_log2;
+    f32x16 acc_dk[2] = {zero16(), zero16()};
+    f32x16 acc_dv[2] = {zero16(), zero16()};
+
+    for (int qt = qt0; qt < n_qt; ++qt) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ld_row + 16 * i;
+            *reinterpret_cast<f32x4 *>(&q_lds[row * kLdsStride + ld_col]) = qpre[i];
+            *reinterpret_cast<f32x4 *>(&do_lds[row * kLdsStride + ld_col]) = dpre[i];
+        }
+        if (tid < kBwdBQ) lse_lds[tid] = stat_pre;
+        else if (tid < 2 * kBwdBQ) dl_lds[tid - kBwdBQ] = stat_pre;
+        __syncthreads();
+        if (qt + 1 < n_qt) prefetch(qt + 1);
+
+        const int q0 = qt * kBwdBQ;
+        if (q0 + kBwdBQ - 1 < kw0 || kw0 >= T) continue;  // all queries precede all keys
+
+        // S and dP (queries x keys) for two 32-query blocks.
+        f32x16 s[2] = {zero16(), zero16()};
+        f32x16 dp[2] = {zero16(), zero16()};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int col = 8 * j + 4 * hf;
+            const f32x4 qa = *reinterpret_cast<const f32x4 *>(&q_lds[l32 * kLdsStride + col]);
+            const f32x4 qb = *reinterpret_cast<const f32x4 *>(&q_lds[(32 + l32) * kLdsStride + col]);
+            const f32x4 da = *reinterpret_cast<const f32x4 *>(&do_lds[l32 * kLdsStride + col]);
+            const f32x4 db = *reinterpret_cast<const f32x4 *>(&do_lds[(32 + l32) * kLdsStride + col]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s[0] = mfma32(qa[c], kr[j][c], s[0]);
+                s[1] = mfma32(qb[c], kr[j][c], s[1]);
+                dp[0] = mfma32(da[c], vr[j][c], dp[0]);
+                dp[1] = mfma32(db[c], vr[j][c], dp[1]);
+            }
+        }
+
+        const bool diag = q0 < kw0 + 31;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lse_lds[32 * qb + 8 * g + 4 * hf]);
+                const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&dl_lds[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int r = 4 * g + c;
+                    float p = fast_exp2(fmaf(s[qb][r], c2, -l4[c]));
+                    if (diag && q0 + 32 * qb + 8 * g + 4 * hf + c < my_k) p = 0.0f;
+                    s[qb][r] = p;                          // P
+                    dp[qb][r] = p * (dp[qb][r] - d4[c]);   // dS
+                }
+            }
+
+        // dV += P^T dO and dK += dS^T Q (keys x dims).
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int row = 32 * qb + 8 * g + 4 * hf + c;
+                    const float d0 = do_lds[row * kLdsStride + l32];
+                    const float d1 = do_lds[row * kLdsStride + 32 + l32];
+                    const float q0v = q_lds[row * kLdsStride + l32];
+                    const float q1v = q_lds[row * kLdsStride + 32 + l32];
+                    acc_dv[0] = mfma32(s[qb][4 * g + c], d0, acc_dv[0]);
+                    acc_dv[1] = mfma32(s[qb][4 * g + c], d1, acc_dv[1]);
+                    acc_dk[0] = mfma32(dp[qb][4 * g + c], q0v, acc_dk[0]);
+                    acc_dk[1] = mfma32(dp[qb][4 * g + c], q1v, acc_dk[1]);
+                }
+    }
+
+    // Accumulator layout (keys x dims): lane -> dim 32*db + l32,
+    // register r -> key kw0 + 8(r/4) + 4hf + r%4.
+    float *dKh = a.dk.p + b * a.dk.sb + h * a.dk.sh;
+    float *dVh = a.dv.p + b * a.dv.sb + h * a.dv.sh;
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+        const int dim = 32 * db + l32;
+        if (dim >= D) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            if (key < T) {
+                dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
+                dVh[key * a.dv.st + dim] = acc_dv[db][r];
+            }
+        }
+    }
+}
+
+void launch_attn_bwd(const BwdParams &p, hipStream_t stream, const hipEvent_t *ev) {
+    const dim3 block(256);
+    const dim3 grid_q(p.nqb * p.bh_pad), grid_k(p.nkb * p.bh_pad);
+    if (ev) hipCheck(hipEventRecord(ev[0], stream));
+    if (p.vec)
+        attn_bwd_dq_kernel<true><<<grid_q, block, 0, stream>>>(p);
+    else
+        attn_bwd_dq_kernel<false><<<grid_q, block, 0, stream>>>(p);
+    hipCheck(hipGetLastError());
+    if (ev) {
+        hipCheck(hipEventRecord(ev[1], stream));
+        hipCheck(hipEventRecord(ev[2], stream));
+    }
+    if (p.vec)
+        attn_bwd_dkdv_kernel<true><<<grid_k, block, 0, stream>>>(p);
+    else
+        attn_bwd_dkdv_kernel<false><<<grid_k, block, 0, stream>>>(p);
+    hipCheck(hipGetLastError());
+    if (ev) hipCheck(hipEventRecord(ev[3], stream));
+}
+
+}  // namespace gptc

@@ -1,0 +1,86 @@
+// Shared device-side pieces of the fused causal attention kernels (gfx950).
+//
+// Fragment layouts of v_mfma_f32_32x32x2_f32 used throughout (wave64):
+//   A (32 x 2):  lane l holds A[l % 32][l / 32]
+//   B (2 x 32):  lane l holds B[l / 32][l % 32]
+//   D (32 x 32): lane l, register r holds D[8*(r/4) + 4*(l/32) + r%4][l % 32]
+// The reduction index of one instruction is split across the two lane
+// halves.  The kernels choose it so that half `hf` of step (g, c) covers
+// row 8g + 4hf + c of a 32-row block: then the 16 accumulator registers of
+// one product are, register for register, the A or B operand of the next
+// product, and no accumulator ever has to be shuffled between lanes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace gptc {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kDPad = 64;          // head size the kernels are built for (D <= 64 is zero-padded)
+constexpr int kLdsStride = 68;     // floats per LDS row: 64 + 4 keeps b128 row reads conflict-free
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element (b, t, h, d) of a per-head view lives at p + b*sb + t*st + h*sh + d.
+// qkv (B, T, 3C):  sb = T*3C, st = 3C, sh = D (k at +C, v at +2C).
+// y / dy (B, T, C): sb = T*C,  st = C,  sh = D.
+// (B, H, T, D):     sb = H*T*D, st = D, sh = T*D.
+struct HeadView {
+    const float *p;
+    uint32_t sb, st, sh;
+};
+struct HeadViewW {
+    float *p;
+    uint32_t sb, st, sh;
+};
+
+__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+    f32x16 z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+    return z;
+}
+
+__device__ __forceinline__ f32x4 zero4() {
+    f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    return z;
+}
+
+// row[dim .. dim+3] with elements at or beyond D read as zero.
+// VEC: D % 4 == 0 and rows 16-byte aligned, so a group is all-in or all-out.
+template <bool VEC>
+__device__ __forceinline__ f32x4 load4(const float *row, int dim, int D) {
+    if (VEC) {
+        if (dim < D) return *reinterpret_cast<const f32x4 *>(row + dim);
+        return zero4();
+    }
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (dim + e < D) ? row[dim + e] : 0.0f;
+    return v;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store4(float *row, int dim, int D, f32x4 v) {
+    if (VEC) {
+        if (dim < D) *reinterpret_cast<f32x4 *>(row + dim) = v;
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (dim + e < D) row[dim + e] = v[e];
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value held by the lane 32 positions away (the other half of the wave).
+__device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32, 64); }
+
+}  // namespace gptc

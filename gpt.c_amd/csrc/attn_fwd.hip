@@ -1,0 +1,207 @@
+// Fused causal attention forward for gfx950: S = QK^T / sqrt(D), causal
+// mask, online softmax and O = PV in one pass; writes O and the row
+// log-sum-exp.  Replaces the permute / batched SGEMM / mask / softmax /
+// batched SGEMM / unpermute sequence of gpt.c
+// (kernels/src/cuda/Attention.cu:170-232; math of
+// kernels/src/cpu/Attention.c:46-167).
+//
+// One workgroup = 4 waves = 128 queries of one (b, h); wave w owns 32
+// queries.  The products are formed transposed, S^T = K Q^T and
+// O^T = V^T P^T, so that each lane owns ONE query (lane % 32) and the
+// softmax row statistics are per-lane scalars: the running max needs one
+// exchange with the other wave half per 64-key tile, the running sum none
+// until the epilogue.  Q stays in registers as the B operand; 64-key K and
+// V tiles are staged in LDS by the whole workgroup and prefetched into
+// registers one tile ahead.
+#include "attn_common.hpp"
+#include "attn_kernels.hpp"
+#include "hip_check.hpp"
+
+namespace gptc {
+
+constexpr int kFwdBM = 128;  // queries per workgroup
+constexpr int kFwdBN = 64;   // keys per LDS tile
+
+template <bool VEC, bool PERM>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
+    __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
+
+    // Longest query blocks first; the (b, h) index runs fastest so that all
+    // query blocks of one head share blockIdx % 8 and hence one XCD's L2.
+    const int bh = blockIdx.x % a.bh_pad;
+    if (bh >= a.B * a.H) return;
+    const int qb = a.nqb - 1 - static_cast<int>(blockIdx.x / a.bh_pad);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int T = a.T, D = a.D;
+
+    const int q_blk0 = qb * kFwdBM;
+    const int qw0 = q_blk0 + 32 * w;
+    const int my_q = qw0 + l32;
+
+    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
+    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
+
+    // Q row of this lane's query, dims 8j + 4hf + c, as B operands.
+    f32x4 qr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        qr[j] = (my_q < T) ? load4<VEC>(Qh + my_q * a.q.st, 8 * j + 4 * hf, D) : zero4();
+    if (PERM && my_q < T) {
+        float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * D;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) store4<VEC>(dst, 8 * j + 4 * hf, D, qr[j]);
+    }
+
+    const int kv_end = min(T, q_blk0 + kFwdBM);
+    const int n_tiles = (kv_end + kFwdBN - 1) / kFwdBN;
+
+    // Cooperative tile load: thread covers rows (tid>>4) + 16i, dims 4*(tid&15).
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    f32x4 kpre[4], vpre[4];
+    auto prefetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = kt * kFwdBN + ld_row + 16 * i;
+            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
+            vpre[i] = (key < T) ? load4<VEC>(Vh + key * a.v.st, ld_col, D) : zero4();
+        }
+    };
+    prefetch(0);
+
+    const float c2 = a.scale_log2;
+    float m_run = -INFINITY;  // running max of s * c2 for this lane's query
+    float l_run = 0.0f;       // this half-wave's share of the running sum
+    f32x16 acc_o[2] = {zero16(), zero16()};
+
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ld_row + 16 * i;
+            *reinterpret_cast<f32x4 *>(&k_lds[row * kLdsStride + ld_col]) = kpre[i];
+            *reinterpret_cast<f32x4 *>(&v_lds[row * kLdsStride + ld_col]) = vpre[i];
+        }
+        if (PERM && kt * kFwdBN >= q_blk0) {
+            // Keys of this workgroup's own block: emit the permuted copies.
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt * kFwdBN + ld_row + 16 * i;
+                if (key < T) {
+                    const uint32_t off = (static_cast<uint32_t>(bh) * T + key) * D;
+                    store4<VEC>(a.kp + off, ld_col, D, kpre[i]);
+                    store4<VEC>(a.vp + off, ld_col, D, vpre[i]);
+                }
+            }
+        }
+        __syncthreads();
+        if (kt + 1 < n_tiles) prefetch(kt + 1);
+
+        const int k0 = kt * kFwdBN;
+        if (k0 > qw0 + 31 || qw0 >= T) continue;  // wave-uniform: tile entirely masked
+
+        // S^T (keys x queries) for two 32-key blocks.
+        f32x16 s[2] = {zero16(), zero16()};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&k_lds[l32 * kLdsStride + 8 * j + 4 * hf]);
+            const f32x4 kb = *reinterpret_cast<const f32x4 *>(&k_lds[(32 + l32) * kLdsStride + 8 * j + 4 * hf]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s[0] = mfma32(ka[c], qr[j][c], s[0]);
+                s[1] = mfma32(kb[c], qr[j][c], s[1]);
+            }
+        }
+
+        if (k0 + kFwdBN - 1 > qw0) {  // tile crosses this wave's diagonal
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (key > my_q) s[kb][r] = -INFINITY;
+                }
+        }
+
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
+        mt = fmaxf(mt, other_half(mt));
+        const float m_new = fmaxf(m_run, mt * c2);
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = fast_exp2(m_run - m_use);
+        float ls = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(fmaf(s[kb][r], c2, -m_use));
+                s[kb][r] = p;
+                ls += p;
+            }
+        l_run = fmaf(l_run, alpha, ls);
+        m_run = m_new;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            acc_o[0][r] *= alpha;
+            acc_o[1][r] *= alpha;
+        }
+
+        // O^T (dims x queries) += V^T P^T; P^T register 4g+c is the B operand.
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int row = 32 * kb + 8 * g + 4 * hf + c;
+                    const float va0 = v_lds[row * kLdsStride + l32];
+                    const float va1 = v_lds[row * kLdsStride + 32 + l32];
+                    acc_o[0] = mfma32(va0, s[kb][4 * g + c], acc_o[0]);
+                    acc_o[1] = mfma32(va1, s[kb][4 * g + c], acc_o[1]);
+                }
+    }
+
+    if (qw0 >= T) return;
+    const float l_tot = l_run + other_half(l_run);
+    if (my_q >= T) return;
+    const float inv = 1.0f / l_tot;
+    float *orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh;
+    float *o2row = a.o2 ? a.o2 + b * a.o.sb + my_q * a.o.st + h * a.o.sh : nullptr;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 val;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) val[c] = acc_o[db][4 * g + c] * inv;
+            const int dim = 32 * db + 8 * g + 4 * hf;
+            store4<VEC>(orow, dim, D, val);
+            if (o2row) store4<VEC>(o2row, dim, D, val);
+        }
+    if (hf == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(l_tot)) * kLn2;
+}
+
+void launch_attn_fwd(const FwdParams &p, hipStream_t stream, const hipEvent_t *ev) {
+    const dim3 grid(p.nqb * p.bh_pad), block(256);
+    const bool vec = p.vec;
+    if (ev) hipCheck(hipEventRecord(ev[0], stream));
+    if (vec && p.qp)
+        attn_fwd_kernel<true, true><<<grid, block, 0, stream>>>(p);
+    else if (vec)
+        attn_fwd_kernel<true, false><<<grid, block, 0, stream>>>(p);
+    else if (p.qp)
+        attn_fwd_kernel<false, true><<<grid, block, 0, stream>>>(p);
+    else
+        attn_fwd_kernel<false, false><<<grid, block, 0, stream>>>(p);
+    hipCheck(hipGetLastError());
+    if (ev) hipCheck(hipEventRecord(ev[1], stream));
+}
+
+}  // namespace gptc

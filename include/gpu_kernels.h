@@ -1,0 +1,100 @@
+/*
+ * gpu_kernels.h -- the C-ABI that this library exports for gpt.c's GPU
+ * device.  Every symbol keeps the name, argument list and meaning of the
+ * CUDA back end it replaces, so gpt.c's device dispatchers
+ * (the files of kernels/src/core/) link against this library instead of
+ * the CUDA objects without a source change.  Plain pointers and sizes only; errors
+ * are fatal (print + exit(EXIT_FAILURE)), as in the reference.
+ *
+ * All device work is ordered on one non-blocking HIP stream created by
+ * runtime_init_cuda().
+ */
+#pragma once
+
+#include <stddef.h>
+#include "tensor.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime: replaces kernels/src/cuda/runtime.h:7-9 (runtime.cu:16-52) ---- */
+void runtime_init_cuda(void);
+void runtime_destroy_cuda(void);
+void synchronize_cuda(void);
+
+/* ---- stream-ordered allocation: replaces kernels/src/cuda/Alloc.h:10-12 ---- */
+void *alloc_cuda(const size_t nbytes);
+void free_cuda(void *ptr);
+
+/* ---- tensor data ops: replace kernels/src/cuda/Tensor.h:9-17 ---- */
+void move_tensor_to_host_cuda(tensor_t *tensor);
+void move_tensor_to_device_cuda(tensor_t *tensor);
+void create_tensor_data_cuda(tensor_t *tensor);
+void zeros_tensor_data_cuda(tensor_t *tensor);
+void ones_tensor_data_cuda(tensor_t *tensor);
+void fill_tensor_data_cuda(tensor_t *tensor, const float value);
+void arange_tensor_data_cuda(tensor_t *tensor, const int start, const int end, const int steps);
+void copy_tensor_data_cuda(tensor_t *dst, const tensor_t *src);
+
+/*
+ * ---- causal self-attention: replaces kernels/src/cuda/Attention.h:9-22 ----
+ *
+ * attention_forward_cuda_kernel(input, mask, n_heads, cache, output)
+ *   input  (B, T, 3C) qkv, device.  output (B, T, C), device, overwritten.
+ *   mask   the layer's (block, block) lower-triangular buffer; block >= T is
+ *          checked.  The kernel applies the causal rule key <= query from
+ *          indices; the buffer itself is never read on the device.
+ *   cache  four device tensors allocated by the caller.  Two layouts are
+ *          accepted and told apart by cache[0]:
+ *          - compact (this library's attention.c): cache[0] IS the input
+ *            tensor (ownership passed to the layer), cache[1] (B, T, C)
+ *            receives a copy of the output, cache[2] (B, H, T) receives the
+ *            row log-sum-exp, cache[3] (B, H, T) is backward scratch;
+ *          - reference (gpt.c's unchanged attention.c:105-120): cache[0..2]
+ *            (B, H, T, D) receive the permuted q, k, v exactly as gpt.c's
+ *            CPU kernel writes them; cache[3], allocated (B, H, T, T), is
+ *            re-pointed to a compact buffer holding the output copy, the
+ *            log-sum-exp and backward scratch (the B*H*T*T probability
+ *            matrix is never formed).
+ *   Supported head sizes: D <= 64 (D = C / n_heads); T <= 65536.
+ *
+ * attention_backward_cuda_kernel(global_grad, cache, n_heads, dout)
+ *   global_grad (B, T, C) upstream gradient (may be clobbered by the caller
+ *   afterwards), cache as left by the forward, dout (B, T, 3C) receives
+ *   dq | dk | dv.  Every element of dout is written (no accumulation), so
+ *   dout need not be zeroed; a zeroed dout (gpt.c attention.c:142-143)
+ *   gives the same result.
+ */
+void attention_forward_cuda_kernel(
+    const tensor_t *input,
+    const tensor_t *mask,
+    const int n_heads,
+    tensor_t **cache,
+    tensor_t *output
+);
+
+void attention_backward_cuda_kernel(
+    const tensor_t *global_grad,
+    tensor_t **cache,
+    const int n_heads,
+    tensor_t *dout
+);
+
+/*
+ * ---- extensions with no counterpart in the reference ----
+ * gptc_stream(): the hipStream_t (as void*) every launch of this library is
+ * ordered on; for callers that time or order their own work against it.
+ *
+ * gptc_set_kernel_events(events, 6): hipEvent_t handles (as void*) that the
+ * attention entry points record on that stream around each kernel launch:
+ * [0,1] the forward kernel, [2,3] the backward dq kernel, [4,5] the
+ * backward dk/dv kernel.  They stay registered until the next call;
+ * events == NULL stops the recording.  For per-kernel timing.
+ */
+void *gptc_stream(void);
+void gptc_set_kernel_events(void **events, int n);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,127 @@
+"""The C-ABI library without a GPU: it loads, exports every function that
+include/*.h declares, keeps tensor_t / attention_t binary-compatible with
+gpt.c, and its host-side logic (constructor, CPU tensor ops, fatal error
+convention) behaves like gpt.c's.  No call here reaches the device.
+"""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+import textwrap
+
+import numpy as np
+import pytest
+
+import gptc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def declared_functions():
+    names = set()
+    for fn in sorted(os.listdir(INCLUDE)):
+        if not fn.endswith(".h"):
+            continue
+        src = open(os.path.join(INCLUDE, fn)).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        src = re.sub(r"//[^\n]*", "", src)
+        src = re.sub(r"#[^\n]*", "", src)
+        src = re.sub(r"typedef\s+(struct|enum)[^;]*?\{.*?\}[^;]*;", "", src, flags=re.S)
+        for m in re.finditer(r"([A-Za-z_][A-Za-z0-9_]*)\s*\([^;{]*\)\s*;", src):
+            names.add(m.group(1))
+    return names - {"if", "while", "for", "return", "sizeof"}
+
+
+def test_every_declared_function_is_exported(lib):
+    names = declared_functions()
+    assert len(names) > 50
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    # The Python front end declares a signature for each of them.
+    assert names <= set(gptc.SIGNATURES), sorted(names - set(gptc.SIGNATURES))
+
+
+def test_struct_layouts_match_gpt_c():
+    # tensor_t: float*, ndims, length, shape[8], to, device; aligned(64) -> 64 bytes.
+    assert ctypes.sizeof(gptc.Tensor) == 64
+    assert gptc.Tensor.device.offset == 56 and gptc.Tensor.shape.offset == 16
+    # attention_t: buffer, cache[4], 7 function pointers, n_embd, n_heads; aligned(64) -> 128.
+    assert gptc.AttentionT.n_heads.offset == 100
+    assert (ctypes.sizeof(gptc.AttentionT) + 63) // 64 * 64 == 128
+
+
+def test_constructor_builds_causal_mask_on_host(lib):
+    rt = gptc.Runtime(lib)
+    layer = gptc.AttentionLayer(rt, 64, 4, 9)
+    buf = layer.buffer.contents
+    assert buf.device == gptc.CPU and buf.ndims == 2 and (buf.shape[0], buf.shape[1]) == (9, 9)
+    mask = rt.to_numpy(layer.buffer)
+    assert np.array_equal(mask, np.tril(np.ones((9, 9), np.float32)))
+    assert layer.num_parameters() == 0
+    assert layer.ptr.contents.n_embd == 64 and layer.ptr.contents.n_heads == 4
+    assert all(not layer.cache(i) for i in range(4))
+    layer.free()
+
+
+def test_cpu_tensor_ops(lib):
+    rt = gptc.Runtime(lib)
+    a = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
+    t = rt.from_numpy(a, gptc.CPU)
+    assert np.array_equal(rt.to_numpy(t), a)
+    shp = (ctypes.c_int * 2)(6, 4)
+    lib.view(t, shp, 2)
+    assert rt.to_numpy(t).shape == (6, 4)
+    buf = ctypes.create_string_buffer(64)
+    lib.shape(t, buf)
+    assert buf.value == b"6, 4"
+    z = lib.zeros((ctypes.c_int * 1)(5), 1, gptc.CPU)
+    o = lib.ones((ctypes.c_int * 1)(5), 1, gptc.CPU)
+    f = lib.fill((ctypes.c_int * 1)(5), 1, ctypes.c_float(2.5), gptc.CPU)
+    r = lib.arange(3, 11, 2, gptc.CPU)
+    assert np.array_equal(rt.to_numpy(z), np.zeros(5))
+    assert np.array_equal(rt.to_numpy(o), np.ones(5))
+    assert np.array_equal(rt.to_numpy(f), np.full(5, 2.5))
+    assert np.array_equal(rt.to_numpy(r), [[3, 5, 7, 9]])
+    c = lib.create_tensor((ctypes.c_int * 2)(6, 4), 2, gptc.CPU)
+    lib.tensor_copy(c, t)
+    assert np.array_equal(rt.to_numpy(c), a.reshape(6, 4))
+    for x in (t, z, o, f, r, c):
+        lib.free_tensor(x)
+
+
+def run_c_snippet(body):
+    """Run a few library calls in a child process (errors are fatal exits)."""
+    code = textwrap.dedent(f"""
+        import ctypes, sys
+        sys.path.insert(0, {os.path.join(ROOT, 'gpt.c_amd')!r})
+        import gptc
+        lib = gptc.load()
+        rt = gptc.Runtime(lib)
+    """) + textwrap.dedent(body)
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+
+
+def test_fatal_error_bad_head_split():
+    r = run_c_snippet("lib.Attention(10, 4, 8)\nprint('survived')")
+    assert r.returncode == 1 and "survived" not in r.stdout
+    assert "divisible by n_heads" in r.stderr and "[ERROR]" in r.stderr
+
+
+def test_fatal_error_cpu_attention_is_not_served():
+    r = run_c_snippet("""
+        import numpy as np
+        layer = gptc.AttentionLayer(rt, 8, 2, 4)
+        x = rt.from_numpy(np.zeros((1, 4, 24), np.float32), gptc.CPU)
+        layer.forward(x)
+        print('survived')
+    """)
+    assert r.returncode == 1 and "survived" not in r.stdout
+    assert "GPU attention path only" in r.stderr
+
+
+def test_fatal_error_gpu_call_before_runtime_init():
+    r = run_c_snippet("lib.alloc_cuda(16)\nprint('survived')")
+    assert r.returncode == 1 and "survived" not in r.stdout
+    assert "runtime_init" in r.stderr

@@ -1,0 +1,206 @@
+"""GPU parity of the fused causal attention against the CPU oracle.
+
+Every case runs the HIP kernels through the library's C-ABI (gpt.c's
+Attention() layer or the attention_*_cuda_kernel entry points directly)
+and compares with the oracle (the C restatement of gpt.c's OpenBLAS CPU
+path) on the same seeded inputs.  Tolerance, from the BASELINE north star:
+max abs err <= 1e-4 on y, dq, dk, dv and the saved log-sum-exp.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import gptc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def qkv_inputs(rt, B, T, C, seed_x=1337, seed_dy=1338):
+    x = rt.normal((B, T, 3 * C), seed_x)
+    dy = rt.normal((B, T, C), seed_dy)
+    return x, dy
+
+
+def run_layer(rt, x, dy, H, block=None):
+    """Forward + backward through Attention() exactly as SelfAttention calls it."""
+    B, T, C3 = x.shape
+    C = C3 // 3
+    layer = gptc.AttentionLayer(rt, C, H, block or T)
+    layer.to(gptc.CUDA)
+    yt = layer.forward(rt.from_numpy(x))
+    y = rt.to_numpy(yt)
+    lse = rt.to_numpy(layer.cache(2)).reshape(B, H, T)
+    dqkv = None
+    if dy is not None:
+        dt = layer.backward(rt.from_numpy(dy))
+        dqkv = rt.to_numpy(dt)
+        rt.free(dt)
+        assert all(not layer.cache(i) for i in range(4))
+    rt.free(yt)
+    layer.free()
+    rt.sync()
+    return y, lse, dqkv
+
+
+def lse_fp64(q, k, heads):
+    """Natural-log row log-sum-exp of the causal scores for (b, h) in heads."""
+    T, D = q.shape[2], q.shape[3]
+    out = {}
+    for b, h in heads:
+        s = q[b, h].astype(np.float64) @ k[b, h].astype(np.float64).T / np.sqrt(D)
+        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
+        m = s.max(-1)
+        out[(b, h)] = m + np.log(np.exp(s - m[:, None]).sum(-1))
+    return out
+
+
+def check(name, got, ref, tol=TOL):
+    err = float(np.abs(got.astype(np.float64) - ref).max()) if got.size else 0.0
+    print(f"  {name}: max abs err {err:.3e}")
+    assert np.isfinite(got).all(), name
+    assert err <= tol, f"{name}: max abs err {err:.3e} > {tol}"
+    return err
+
+
+def compare_with_oracle(rt, oracle, B, T, C, H, backward=True, block=None, sample_heads=None):
+    x, dy = qkv_inputs(rt, B, T, C)
+    y, lse, dqkv = run_layer(rt, x, dy if backward else None, H, block)
+    y_ref, q, k, v, att = oracle.forward(x, H)
+    print(f"case B={B} T={T} C={C} H={H} D={C // H}")
+    check("y", y, y_ref)
+    heads = sample_heads or [(b, h) for b in range(B) for h in range(H)]
+    for (b, h), ref in lse_fp64(q, k, heads).items():
+        check(f"lse[{b},{h}]", lse[b, h], ref)
+    if backward:
+        d_ref = oracle.backward(dy, H, q, k, v, att)
+        check("dq", dqkv[..., :C], d_ref[..., :C])
+        check("dk", dqkv[..., C:2 * C], d_ref[..., C:2 * C])
+        check("dv", dqkv[..., 2 * C:], d_ref[..., 2 * C:])
+
+
+SMALL = [  # (B, T, C, H)
+    (1, 1, 64, 1),
+    (2, 17, 192, 3),
+    (1, 64, 128, 2),
+    (2, 100, 256, 4),
+    (1, 129, 128, 2),      # crosses a 128-query block
+    (1, 200, 64, 2),       # D = 32
+    (2, 5, 6, 2),          # D = 3 (gpt.c's tests/test_self_attention.c shape class)
+    (2, 16, 16, 2),        # D = 8
+    (1, 70, 100, 25),      # H = 25, D = 4
+    (1, 257, 48, 1),       # D = 48
+    (2, 300, 48, 3),       # D = 16
+    (1, 511, 768, 12),     # C4's longest window shape at B = 1
+]
+
+
+@pytest.mark.parametrize("B,T,C,H", SMALL)
+def test_small_shapes_fwd_bwd(rt, oracle, B, T, C, H):
+    compare_with_oracle(rt, oracle, B, T, C, H)
+
+
+def test_mask_block_larger_than_T(rt, oracle):
+    compare_with_oracle(rt, oracle, 2, 77, 128, 2, block=1024)
+
+
+def test_c1_forward_b8_t128_h12(rt, oracle):
+    compare_with_oracle(rt, oracle, 8, 128, 768, 12, backward=False)
+
+
+def test_c2_fwd_bwd_b8_t1024_h12(rt, oracle):
+    compare_with_oracle(rt, oracle, 8, 1024, 768, 12, sample_heads=[(0, 0), (3, 7), (7, 11)])
+
+
+def test_c5_fwd_bwd_b4_t1024_h25(rt, oracle):
+    compare_with_oracle(rt, oracle, 4, 1024, 1600, 25, sample_heads=[(0, 0), (2, 13), (3, 24)])
+
+
+def test_reference_cache_layout(rt, oracle):
+    """gpt.c's unchanged attention.c allocates q, k, v (B,H,T,D) and att (B,H,T,T)
+    caches (attention.c:105-120) and passes a zeroed dout: the entry points
+    must serve that layout too, leaving the same q, k, v the CPU kernel caches."""
+    lib = rt.lib
+    for B, T, C, H in [(2, 150, 256, 4), (2, 5, 6, 2)]:
+        D = C // H
+        x, dy = qkv_inputs(rt, B, T, C, 7, 8)
+        xt = rt.from_numpy(x)
+        mask = rt.from_numpy(np.tril(np.ones((T, T), np.float32)))
+        caches = (gptc.TensorP * 4)(*[rt.empty((B, H, T, D)) for _ in range(3)], rt.empty((B, H, T, T)))
+        yt = rt.empty((B, T, C))
+        lib.attention_forward_dispatch(xt, mask, H, caches, yt)
+        y = rt.to_numpy(yt)
+        rt.free(xt)  # attention.c:123 frees the input right after the call
+        y_ref, q, k, v, att = oracle.forward(x, H)
+        check("y", y, y_ref)
+        for i, ref in enumerate((q, k, v)):
+            assert np.array_equal(rt.to_numpy(caches[i]), ref), f"cache[{i}]"
+        dyt = rt.from_numpy(dy)
+        dout = lib.zeros((ctypes.c_int * 3)(B, T, 3 * C), 3, gptc.CUDA)
+        lib.attention_backward_dispatch(dyt, caches, H, dout)
+        d = rt.to_numpy(dout)
+        d_ref = oracle.backward(dy, H, q, k, v, att)
+        check("dqkv", d, d_ref)
+        for t in (yt, dyt, dout, mask, *caches):
+            rt.free(t)
+        rt.sync()
+
+
+def test_deterministic(rt):
+    x, dy = qkv_inputs(rt, 2, 300, 256, 11, 12)
+    a = run_layer(rt, x, dy, 4)
+    b = run_layer(rt, x, dy, 4)
+    for u, w in zip(a, b):
+        assert np.array_equal(u, w)
+
+
+def test_causality_at_full_length(rt):
+    B, T, C, H = 2, 1024, 768, 12
+    x, dy = qkv_inputs(rt, B, T, C, 21, 22)
+    y, _, d = run_layer(rt, x, dy, H)
+    x2 = x.copy()
+    x2[:, 600:] = rt.normal((B, T - 600, 3 * C), 23)
+    y2, _, d2 = run_layer(rt, x2, dy, H)
+    assert np.array_equal(y[:, :600], y2[:, :600])
+    assert np.array_equal(d[:, :600, :C], d2[:, :600, :C])
+    assert not np.array_equal(y[:, 600:], y2[:, 600:])
+
+
+def test_forward_twice_then_backward(rt, oracle):
+    """A second forward without backward drops the first cache (no leak, no mix-up)."""
+    B, T, C, H = 1, 90, 128, 2
+    layer = gptc.AttentionLayer(rt, C, H, T)
+    layer.to(gptc.CUDA)
+    x1, _ = qkv_inputs(rt, B, T, C, 31, 32)
+    x2, dy = qkv_inputs(rt, B, T, C, 33, 34)
+    rt.free(layer.forward(rt.from_numpy(x1)))
+    yt = layer.forward(rt.from_numpy(x2))
+    dt = layer.backward(rt.from_numpy(dy))
+    y_ref, q, k, v, att = oracle.forward(x2, H)
+    check("y", rt.to_numpy(yt), y_ref)
+    check("dqkv", rt.to_numpy(dt), oracle.backward(dy, H, q, k, v, att))
+    rt.free(yt)
+    rt.free(dt)
+    layer.free()
+    rt.sync()
+
+
+def test_device_tensor_ops(rt):
+    lib = rt.lib
+    a = rt.normal((3, 1001), 5)
+    t = rt.from_numpy(a)
+    assert np.array_equal(rt.to_numpy(t), a)
+    c = rt.empty((3, 1001))
+    lib.tensor_copy(c, t)
+    assert np.array_equal(rt.to_numpy(c), a)
+    f = lib.fill((ctypes.c_int * 1)(1003), 1, ctypes.c_float(-1.5), gptc.CUDA)
+    z = lib.zeros((ctypes.c_int * 1)(7), 1, gptc.CUDA)
+    r = lib.arange(2, 20, 3, gptc.CUDA)
+    assert np.array_equal(rt.to_numpy(f), np.full(1003, -1.5, np.float32))
+    assert np.array_equal(rt.to_numpy(z), np.zeros(7, np.float32))
+    assert np.array_equal(rt.to_numpy(r), [[2, 5, 8, 11, 14, 17]])
+    for x in (t, c, f, z, r):
+        rt.free(x)
+    rt.sync()
