@@ -144,12 +144,45 @@ def cpu_baseline(cfg, x, dy, budget_s):
     }
 
 
+def copy_calibration(args):
+    """Plain device copy of a known size through copy_tensor_data_cuda.
+
+    Used to scale rocprof's FETCH_SIZE / WRITE_SIZE counters (a copy of N
+    bytes must fetch N and write N) and as the achievable-bandwidth check.
+    """
+    n = 64 << 20  # floats: 256 MiB per buffer, larger than the 256 MB MALL
+    lib = gptc.load()
+    rt = gptc.Runtime(lib)
+    rt.init()
+    hip = Hip()
+    src = lib.fill((ctypes.c_int * 1)(n), 1, ctypes.c_float(1.0), gptc.CUDA)
+    dst = rt.empty((n,))
+    for _ in range(args.warmup):
+        lib.tensor_copy(dst, src)
+    rt.sync()
+    a, b = hip.event(), hip.event()
+    hip.record(a, rt.stream())
+    for _ in range(args.steps):
+        lib.tensor_copy(dst, src)
+    hip.record(b, rt.stream())
+    ms = hip.elapsed_ms(a, b) / args.steps
+    nbytes = 4 * n
+    print(json.dumps({"workload": "copy", "bytes_read_per_launch": nbytes, "bytes_written_per_launch": nbytes,
+                      "ms_per_launch": round(ms, 5), "GB_per_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1),
+                      "hbm_peak_GB_per_s": HBM_PEAK_GBS}), flush=True)
+    rt.free(src)
+    rt.free(dst)
+    rt.sync()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
+    ap.add_argument("--workload", choices=["attention", "copy"], default="attention",
+                    help="copy: HBM copy of known size, to calibrate rocprof byte counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
@@ -158,6 +191,9 @@ def main():
         print("bench.py: this build measures one GPU only (every (b, h) pair of causal attention is "
               "independent; see DESIGN.md for how the path shards). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "copy":
+        copy_calibration(args)
+        return
 
     cfg = CONFIGS[args.config]
     B, T, C, H = cfg["B"], cfg["T"], cfg["C"], cfg["H"]
@@ -189,12 +225,14 @@ def main():
     rt.sync()
     hip.device_sync()
 
-    evs = [[hip.event() for _ in range(6)] for _ in range(args.steps)]
-    ev_arrays = [(ctypes.c_void_p * 6)(*e) for e in evs]
+    kernels = ("fwd", "bwd_delta", "bwd_dkdv", "bwd_dq")
+    n_ev = 2 * len(kernels)
+    evs = [[hip.event() for _ in range(n_ev)] for _ in range(args.steps)]
+    ev_arrays = [(ctypes.c_void_p * n_ev)(*e) for e in evs]
     t_begin, t_end = hip.event(), hip.event()
     hip.record(t_begin, stream)
     for i in range(args.steps):
-        lib.gptc_set_kernel_events(ev_arrays[i], 6)
+        lib.gptc_set_kernel_events(ev_arrays[i], n_ev)
         step()
     hip.record(t_end, stream)
     rt.sync()
@@ -202,14 +240,16 @@ def main():
     lib.gptc_set_kernel_events(None, 0)
     total_ms = hip.elapsed_ms(t_begin, t_end)
     k_ms = {name: statistics.mean(hip.elapsed_ms(e[2 * j], e[2 * j + 1]) for e in evs)
-            for j, name in enumerate(("fwd", "bwd_dq", "bwd_dkdv"))}
+            for j, name in enumerate(kernels)}
     ms_per_step = total_ms / args.steps
 
     unit = contraction_flops(B, T, H, D)
     flops = 6 * unit
     peak, cu, mhz, peak_src = device_peak()
     value = flops / (ms_per_step * 1e-3) / 1e12
-    kernel_flops = {"fwd": 2 * unit, "bwd_dq": 1 * unit, "bwd_dkdv": 3 * unit}
+    # Algorithmic contractions per kernel: forward S and PV; dk/dv kernel dP,
+    # dV, dK; dq kernel dQ (the delta kernel does no contraction).
+    kernel_flops = {"fwd": 2 * unit, "bwd_delta": 0.0, "bwd_dkdv": 3 * unit, "bwd_dq": 1 * unit}
     dom = max(k_ms, key=k_ms.get)
     achieved = kernel_flops[dom] / (k_ms[dom] * 1e-3) / 1e12
     log(f"[bench] {ms_per_step:.4f} ms/step, {value:.2f} TFLOP/s; kernels (ms): " +

@@ -63,8 +63,9 @@ int64_t packed_state_len(const Dims &d) {
 }
 
 // Events registered by gptc_set_kernel_events: [0,1] around the forward
-// kernel, [2,3] around the dq kernel, [4,5] around the dk/dv kernel.
-hipEvent_t g_events[6];
+// kernel, then [2,3] delta, [4,5] dk/dv and [6,7] dq of the backward.
+constexpr int kNumEvents = 8;
+hipEvent_t g_events[kNumEvents];
 bool g_have_events = false;
 
 }  // namespace
@@ -74,8 +75,10 @@ extern "C" void gptc_set_kernel_events(void **events, int n) {
         g_have_events = false;
         return;
     }
-    CHECK_ERROR(n != 6, "Expected 6 events (forward, dq, dk/dv; start and end of each), but got %d.", n);
-    for (int i = 0; i < 6; i++) g_events[i] = static_cast<hipEvent_t>(events[i]);
+    CHECK_ERROR(n != kNumEvents,
+                "Expected %d events (start and end of forward, delta, dk/dv and dq kernels), but got %d.",
+                kNumEvents, n);
+    for (int i = 0; i < kNumEvents; i++) g_events[i] = static_cast<hipEvent_t>(events[i]);
     g_have_events = true;
 }
 
@@ -215,8 +218,14 @@ extern "C" void attention_backward_cuda_kernel(const tensor_t *global_grad, tens
     p.scale_log2 = gptc::kLog2e * p.scale;
     p.nqb = (d.T + 127) / 128;
     p.nkb = (d.T + 127) / 128;
+    p.nqt = (d.T + 63) / 64;
     p.bh_pad = bh_padded(d.B * d.H);
     p.vec = (d.D % 4 == 0) && aligned16(p.q.p) && aligned16(p.k.p) && aligned16(p.v.p) && aligned16(state) &&
             aligned16(global_grad->t) && aligned16(dout->t);
+
+    // dS scratch: stream-ordered, released right after the kernels that use it.
+    const size_t ds_floats = gptc::bwd_ds_floats(d.B, d.H, d.T);
+    p.ds = static_cast<float *>(alloc_cuda(ds_floats * sizeof(float)));
     gptc::launch_attn_bwd(p, gptc_stream_checked(), g_have_events ? g_events + 2 : nullptr);
+    free_cuda(p.ds);
 }

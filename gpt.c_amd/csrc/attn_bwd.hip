@@ -1,164 +1,64 @@
-// Fused causal attention backward for gfx950 (FlashAttention-2 style:
-// P is rebuilt from the saved log-sum-exp, never stored).  Replaces
-// gpt.c's unpermute / 4 batched SGEMMs / softmax backward / permute
-// sequence (kernels/src/cuda/Attention.cu:235-324; math of
+// Fused causal attention backward for gfx950 (FlashAttention-2 style: P is
+// rebuilt from the saved log-sum-exp, never stored).  Replaces gpt.c's
+// unpermute / 4 batched SGEMMs / softmax backward / permute sequence
+// (kernels/src/cuda/Attention.cu:235-324; math of
 // kernels/src/cpu/Attention.c:169-301):
 //     dP = dO V^T,  dV = P^T dO,  dS = P o (dP - rowsum(dP o P)),
 //     dQ = dS K / sqrt(D),  dK = dS^T Q / sqrt(D),
 // using rowsum(dP o P) = rowsum(dO o O) =: delta.
 //
-// Two kernels, each writing its outputs exactly once (no atomics, no
-// zeroed output needed, deterministic):
-//   attn_bwd_dq_kernel    query-parallel (like the forward): per 32-query
-//                         wave, S^T, dP^T, dS^T over the key tiles and
-//                         dQ^T += K^T dS^T.  Also computes delta from dO
-//                         and O and stores it for the second kernel.
-//   attn_bwd_dkdv_kernel  key-parallel: per 32-key wave (K, V resident in
-//                         registers), S, dP, dS over the query tiles and
-//                         dV += P^T dO, dK += dS^T Q.
-// In both, the accumulator of the score product is directly the operand
-// of the gradient products (see the layout note in attn_common.hpp).
+// Three kernels; every output element is written exactly once (no atomics,
+// no zeroed output needed, bit-for-bit deterministic):
+//   attn_bwd_delta_kernel  delta = rowsum(dO o O); streams dO and O once.
+//   attn_bwd_dkdv_kernel   key-parallel: per 32-key wave (K, V resident in
+//                          registers), over the query tiles: S, P, dP, dS,
+//                          dV += P^T dO, dK += dS^T Q.  It also stores the
+//                          causal tiles of dS, in the exact register layout
+//                          the dq kernel consumes them in.
+//   attn_bwd_dq_kernel     query-parallel: dQ^T += K^T dS^T, one
+//                          contraction per tile instead of recomputing S
+//                          and dP (two more contractions).
+// The accumulator of the score product is directly the operand of the
+// gradient products (see the layout note in attn_common.hpp).
 #include "attn_common.hpp"
 #include "attn_kernels.hpp"
 #include "hip_check.hpp"
 
 namespace gptc {
 
-constexpr int kBwdBM = 128;  // queries per dq workgroup (32 per wave)
-constexpr int kBwdBN = 64;   // keys per LDS tile in the dq kernel
 constexpr int kBwdBK = 128;  // keys per dk/dv workgroup (32 per wave)
 constexpr int kBwdBQ = 64;   // queries per LDS tile in the dk/dv kernel
+constexpr int kBwdBM = 128;  // queries per dq workgroup (32 per wave)
+constexpr int kBwdBN = 64;   // keys per LDS tile in the dq kernel
 
+// ---- delta = rowsum(dO o O): 16 lanes per (b, t, h) row, 16 rows per workgroup ----
 template <bool VEC>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
-    __shared__ __attribute__((aligned(16))) float k_lds[kBwdBN * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float v_lds[kBwdBN * kLdsStride];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
-    const int bh = blockIdx.x % a.bh_pad;
-    if (bh >= a.B * a.H) return;
-    const int qb = a.nqb - 1 - static_cast<int>(blockIdx.x / a.bh_pad);
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int T = a.T, D = a.D;
-
-    const int q_blk0 = qb * kBwdBM;
-    const int qw0 = q_blk0 + 32 * w;
-    const int my_q = qw0 + l32;
-    const bool q_ok = my_q < T;
-
-    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
-    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
-    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
-    const float *Orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh;
-    const float *dOrow = a.dout.p + b * a.dout.sb + my_q * a.dout.st + h * a.dout.sh;
-
-    f32x4 qr[8], dr[8];
-    float dsum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int dim = 8 * j + 4 * hf;
-        qr[j] = q_ok ? load4<VEC>(Qh + my_q * a.q.st, dim, D) : zero4();
-        dr[j] = q_ok ? load4<VEC>(dOrow, dim, D) : zero4();
-        const f32x4 orj = q_ok ? load4<VEC>(Orow, dim, D) : zero4();
-#pragma unroll
-        for (int c = 0; c < 4; ++c) dsum = fmaf(dr[j][c], orj[c], dsum);
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) {
+    const int l16 = threadIdx.x & 15;
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4);  // (b*T + t)*H + h: memory order of (B, T, C)
+    const int rows = a.B * a.T * a.H;
+    float sum = 0.0f;
+    int b = 0, t = 0, h = 0;
+    if (row < rows) {
+        h = row % a.H;
+        const int bt = row / a.H;
+        t = bt % a.T;
+        b = bt / a.T;
+        const float *o = a.o.p + b * a.o.sb + t * a.o.st + h * a.o.sh;
+        const float *g = a.dout.p + b * a.dout.sb + t * a.dout.st + h * a.dout.sh;
+        if (VEC) {
+            const f32x4 x = load4<true>(o, 4 * l16, a.D), y = load4<true>(g, 4 * l16, a.D);
+            sum = x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+        } else {
+            for (int d = l16; d < a.D; d += 16) sum = fmaf(o[d], g[d], sum);
+        }
     }
-    const float delta = dsum + other_half(dsum);
-    const uint32_t stat = static_cast<uint32_t>(bh) * T + my_q;
-    if (q_ok && hf == 0) a.delta[stat] = delta;
-    const float lse2 = q_ok ? a.lse[stat] * kLog2e : 0.0f;
-
-    const int kv_end = min(T, q_blk0 + kBwdBM);
-    const int n_tiles = (kv_end + kBwdBN - 1) / kBwdBN;
-    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
-    f32x4 kpre[4], vpre[4];
-    auto prefetch = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = kt * kBwdBN + ld_row + 16 * i;
-            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
-            vpre[i] = (key < T) ? load4<VEC>(Vh + key * a.v.st, ld_col, D) : zero4();
-        }
-    };
-    prefetch(0);
-
-    const float c2 = a.scale_log2;
-    f32x16 acc_dq[2] = {zero16(), zero16()};
-
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = ld_row + 16 * i;
-            *reinterpret_cast<f32x4 *>(&k_lds[row * kLdsStride + ld_col]) = kpre[i];
-            *reinterpret_cast<f32x4 *>(&v_lds[row * kLdsStride + ld_col]) = vpre[i];
-        }
-        __syncthreads();
-        if (kt + 1 < n_tiles) prefetch(kt + 1);
-
-        const int k0 = kt * kBwdBN;
-        if (k0 > qw0 + 31 || qw0 >= T) continue;
-
-        f32x16 s[2] = {zero16(), zero16()};
-        f32x16 dp[2] = {zero16(), zero16()};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int col = 8 * j + 4 * hf;
-            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&k_lds[l32 * kLdsStride + col]);
-            const f32x4 kb = *reinterpret_cast<const f32x4 *>(&k_lds[(32 + l32) * kLdsStride + col]);
-            const f32x4 va = *reinterpret_cast<const f32x4 *>(&v_lds[l32 * kLdsStride + col]);
-            const f32x4 vb = *reinterpret_cast<const f32x4 *>(&v_lds[(32 + l32) * kLdsStride + col]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                s[0] = mfma32(ka[c], qr[j][c], s[0]);
-                s[1] = mfma32(kb[c], qr[j][c], s[1]);
-                dp[0] = mfma32(va[c], dr[j][c], dp[0]);
-                dp[1] = mfma32(vb[c], dr[j][c], dp[1]);
-            }
-        }
-
-        const bool diag = k0 + kBwdBN - 1 > qw0;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float p = fast_exp2(fmaf(s[kb][r], c2, -lse2));
-                if (diag) {
-                    const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-                    if (key > my_q) p = 0.0f;
-                }
-                s[kb][r] = p * (dp[kb][r] - delta);  // dS^T
-            }
-
-        // dQ^T (dims x queries) += K^T dS^T
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int row = 32 * kb + 8 * g + 4 * hf + c;
-                    const float ka0 = k_lds[row * kLdsStride + l32];
-                    const float ka1 = k_lds[row * kLdsStride + 32 + l32];
-                    acc_dq[0] = mfma32(ka0, s[kb][4 * g + c], acc_dq[0]);
-                    acc_dq[1] = mfma32(ka1, s[kb][4 * g + c], acc_dq[1]);
-                }
-    }
-
-    if (!q_ok) return;
-    float *dqrow = a.dq.p + b * a.dq.sb + my_q * a.dq.st + h * a.dq.sh;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            f32x4 val;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) val[c] = acc_dq[db][4 * g + c] * a.scale;
-            store4<VEC>(dqrow, 32 * db + 8 * g + 4 * hf, D, val);
-        }
+    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    if (row < rows && l16 == 0) a.delta[(static_cast<uint32_t>(b) * a.H + h) * a.T + t] = sum;
 }
 
+// ---- dK, dV (and the dS tiles) ----
 template <bool VEC>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
     __shared__ __attribute__((aligned(16))) float q_lds[kBwdBQ * kLdsStride];
@@ -196,7 +96,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
     }
 
     const int qt0 = k_blk0 / kBwdBQ;
-    const int n_qt = (T + kBwdBQ - 1) / kBwdBQ;
+    const int n_qt = a.nqt;
     const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
     f32x4 qpre[4], dpre[4];
     float stat_pre = 0.0f;
@@ -272,6 +172,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
                 }
             }
 
+        // Hand dS to the dq kernel: block (qt, key block kw0/32), [64 queries][32 keys].
+        float *dsb = a.ds + ds_block_offset(bh, a.nqt, qt, kw0 >> 5);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                dsb[(32 * qb + 8 * (r >> 2) + 4 * hf + (r & 3)) * 32 + l32] = dp[qb][r];
+
         // dV += P^T dO and dK += dS^T Q (keys x dims).
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -310,14 +218,112 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
     }
 }
 
+// ---- dQ = dS K / sqrt(D) from the stored dS tiles ----
+template <bool VEC>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
+    __shared__ __attribute__((aligned(16))) float k_lds[kBwdBN * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
+    const int bh = blockIdx.x % a.bh_pad;
+    if (bh >= a.B * a.H) return;
+    const int qb = a.nqb - 1 - static_cast<int>(blockIdx.x / a.bh_pad);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int T = a.T, D = a.D;
+
+    const int q_blk0 = qb * kBwdBM;
+    const int qw0 = q_blk0 + 32 * w;
+    const int my_q = qw0 + l32;
+    const bool wave_on = qw0 < T;
+
+    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+    // This lane's dS row (query my_q) inside its 64-query tile: key block kb32
+    // starts kb32 * 2048 floats further; keys 8g + 4hf + c come as float4 g.
+    const int qt = qw0 >> 6;
+    const float *ds_row = a.ds + ds_block_offset(bh, a.nqt, qt, 0) + ((qw0 & 32) + l32) * 32 + 4 * hf;
+
+    const int kv_end = min(T, q_blk0 + kBwdBM);
+    const int n_tiles = (kv_end + kBwdBN - 1) / kBwdBN;
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    f32x4 kpre[4];
+    f32x4 dsn[2][4];
+    auto prefetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = kt * kBwdBN + ld_row + 16 * i;
+            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
+        }
+        // Tiles past this wave's diagonal and key blocks wholly past T were
+        // never written: read nothing from them.
+        const bool on = wave_on && kt * kBwdBN <= qw0 + 31;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int kb32 = 2 * kt + kb;
+            const bool ok = on && 32 * kb32 < T;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                dsn[kb][g] = ok ? *reinterpret_cast<const f32x4 *>(ds_row + kb32 * kDsBlock + 8 * g) : zero4();
+        }
+    };
+    prefetch(0);
+
+    f32x16 acc_dq[2] = {zero16(), zero16()};
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<f32x4 *>(&k_lds[(ld_row + 16 * i) * kLdsStride + ld_col]) = kpre[i];
+        __syncthreads();
+        f32x4 dsc[2][4];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) dsc[kb][g] = dsn[kb][g];
+        if (kt + 1 < n_tiles) prefetch(kt + 1);
+
+        if (!wave_on || kt * kBwdBN > qw0 + 31) continue;
+        // dQ^T (dims x queries) += K^T dS^T
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int row = 32 * kb + 8 * g + 4 * hf + c;
+                    const float ka0 = k_lds[row * kLdsStride + l32];
+                    const float ka1 = k_lds[row * kLdsStride + 32 + l32];
+                    acc_dq[0] = mfma32(ka0, dsc[kb][g][c], acc_dq[0]);
+                    acc_dq[1] = mfma32(ka1, dsc[kb][g][c], acc_dq[1]);
+                }
+    }
+
+    if (my_q >= T) return;
+    float *dqrow = a.dq.p + b * a.dq.sb + my_q * a.dq.st + h * a.dq.sh;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 val;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) val[c] = acc_dq[db][4 * g + c] * a.scale;
+            store4<VEC>(dqrow, 32 * db + 8 * g + 4 * hf, D, val);
+        }
+}
+
+size_t bwd_ds_floats(int B, int H, int T) {
+    const size_t nqt = (T + kBwdBQ - 1) / kBwdBQ;
+    return static_cast<size_t>(B) * H * nqt * (nqt + 1) * kDsBlock;
+}
+
 void launch_attn_bwd(const BwdParams &p, hipStream_t stream, const hipEvent_t *ev) {
     const dim3 block(256);
-    const dim3 grid_q(p.nqb * p.bh_pad), grid_k(p.nkb * p.bh_pad);
+    const int rows = p.B * p.T * p.H;
+    const dim3 grid_d((rows + 15) / 16), grid_k(p.nkb * p.bh_pad), grid_q(p.nqb * p.bh_pad);
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
     if (p.vec)
-        attn_bwd_dq_kernel<true><<<grid_q, block, 0, stream>>>(p);
+        attn_bwd_delta_kernel<true><<<grid_d, block, 0, stream>>>(p);
     else
-        attn_bwd_dq_kernel<false><<<grid_q, block, 0, stream>>>(p);
+        attn_bwd_delta_kernel<false><<<grid_d, block, 0, stream>>>(p);
     hipCheck(hipGetLastError());
     if (ev) {
         hipCheck(hipEventRecord(ev[1], stream));
@@ -328,7 +334,16 @@ void launch_attn_bwd(const BwdParams &p, hipStream_t stream, const hipEvent_t *e
     else
         attn_bwd_dkdv_kernel<false><<<grid_k, block, 0, stream>>>(p);
     hipCheck(hipGetLastError());
-    if (ev) hipCheck(hipEventRecord(ev[3], stream));
+    if (ev) {
+        hipCheck(hipEventRecord(ev[3], stream));
+        hipCheck(hipEventRecord(ev[4], stream));
+    }
+    if (p.vec)
+        attn_bwd_dq_kernel<true><<<grid_q, block, 0, stream>>>(p);
+    else
+        attn_bwd_dq_kernel<false><<<grid_q, block, 0, stream>>>(p);
+    hipCheck(hipGetLastError());
+    if (ev) hipCheck(hipEventRecord(ev[5], stream));
 }
 
 }  // namespace gptc

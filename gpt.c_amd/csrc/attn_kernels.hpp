@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <cstddef>
 #include "attn_common.hpp"
 
 namespace gptc {
@@ -24,20 +25,34 @@ struct BwdParams {
     HeadView o;           // saved y
     HeadView dout;        // upstream gradient dy (B, T, C)
     const float *lse;     // (B, H, T)
-    float *delta;         // (B, H, T) rowsum(dy * y), written by the dq kernel
+    float *delta;         // (B, H, T) rowsum(dy * y), written by the delta kernel
+    float *ds;            // dS scratch, bwd_ds_floats(B, H, T) floats (packed causal tiles)
     HeadViewW dq, dk, dv; // slices of dqkv (B, T, 3C)
     int B, H, T, D;
     float scale_log2;     // log2(e) / sqrt(D)
     float scale;          // 1 / sqrt(D)
     int nqb;              // ceil(T / 128) query blocks (dq kernel)
     int nkb;              // ceil(T / 128) key blocks (dk/dv kernel)
+    int nqt;              // ceil(T / 64) query tiles of the dS store
     int bh_pad;
     bool vec;
 };
 
+// Stored dS: per (b, h), for each 64-query tile qt the 32-key blocks
+// kb32 = 0 .. 2qt+1 (all that the causal rule leaves non-zero) follow one
+// another; block (qt, kb32) is a row-major [64 queries][32 keys] array.
+constexpr int kDsBlock = 64 * 32;
+
+__host__ __device__ inline size_t ds_block_offset(int bh, int nqt, int qt, int kb32) {
+    return (static_cast<size_t>(bh) * nqt * (nqt + 1) + static_cast<size_t>(qt) * (qt + 1) + kb32) * kDsBlock;
+}
+
+size_t bwd_ds_floats(int B, int H, int T);
+
 // ev: optional events recorded on `stream` around each kernel launch
-// (forward: ev[0], ev[1]; backward: ev[0..1] around the dq kernel and
-// ev[2..3] around the dk/dv kernel).  nullptr: no events.
+// (forward: ev[0], ev[1]; backward: ev[0..1] around the delta kernel,
+// ev[2..3] around the dk/dv kernel, ev[4..5] around the dq kernel).
+// nullptr: no events.
 void launch_attn_fwd(const FwdParams &p, hipStream_t stream, const hipEvent_t *ev);
 void launch_attn_bwd(const BwdParams &p, hipStream_t stream, const hipEvent_t *ev);
 

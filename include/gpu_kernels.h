@@ -86,10 +86,10 @@ void attention_backward_cuda_kernel(
  * gptc_stream(): the hipStream_t (as void*) every launch of this library is
  * ordered on; for callers that time or order their own work against it.
  *
- * gptc_set_kernel_events(events, 6): hipEvent_t handles (as void*) that the
+ * gptc_set_kernel_events(events, 8): hipEvent_t handles (as void*) that the
  * attention entry points record on that stream around each kernel launch:
- * [0,1] the forward kernel, [2,3] the backward dq kernel, [4,5] the
- * backward dk/dv kernel.  They stay registered until the next call;
+ * [0,1] the forward kernel, then the backward's [2,3] delta, [4,5] dk/dv
+ * and [6,7] dq kernels.  They stay registered until the next call;
  * events == NULL stops the recording.  For per-kernel timing.
  */
 void *gptc_stream(void);
