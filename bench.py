@@ -286,6 +286,17 @@ def main():
             "algorithmic_flop_per_launch": kernel_flops[dom],
         },
     }
+    # HBM bytes per launch of the dominant kernel, from the committed rocprof
+    # byte-counter runs (scaled by a plain copy; see profiles/).
+    traffic_file = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.config}.json")
+    kernel_symbol = {"fwd": "attn_fwd_kernel", "bwd_delta": "attn_bwd_delta_kernel",
+                     "bwd_dkdv": "attn_bwd_dkdv_kernel", "bwd_dq": "attn_bwd_dq_kernel"}[dom]
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            tr = json.load(f)["kernels"].get(kernel_symbol)
+        if tr:
+            result["roofline"]["traffic"] = tr["read_bytes"] + tr["write_bytes"]
+            result["roofline"]["traffic_source"] = f"profiles/hbm_traffic_{args.config}.json (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE)"
     for t in (dyt, mask, yt, dqkv, *caches):
         rt.free(t)
     rt.sync()
