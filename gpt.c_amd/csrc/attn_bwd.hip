@@ -60,7 +60,8 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) 
 
 // ---- dK, dV (and the dS tiles) ----
 template <bool VEC>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_kernel(
+    const BwdParams a) {
     __shared__ __attribute__((aligned(16))) float q_lds[kBwdBQ * kLdsStride];
     __shared__ __attribute__((aligned(16))) float do_lds[kBwdBQ * kLdsStride];
     __shared__ __attribute__((aligned(16))) float lse_lds[kBwdBQ];
@@ -134,30 +135,29 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
         if (qt + 1 < n_qt) prefetch(qt + 1);
 
         const int q0 = qt * kBwdBQ;
-        if (q0 + kBwdBQ - 1 < kw0 || kw0 >= T) continue;  // all queries precede all keys
+        float *dsb = a.ds + ds_block_offset(bh, a.nqt, qt, kw0 >> 5);
+        // The tile's two 32-query halves one after the other: one S and one dP
+        // accumulator live at a time, which keeps the wave within the register
+        // budget of two waves per SIMD.
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qh0 = q0 + 32 * qb;
+            if (qh0 + 31 < kw0 || kw0 >= T) continue;  // all queries precede all keys
 
-        // S and dP (queries x keys) for two 32-query blocks.
-        f32x16 s[2] = {zero16(), zero16()};
-        f32x16 dp[2] = {zero16(), zero16()};
+            // S and dP (queries x keys) for this 32-query half.
+            f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int col = 8 * j + 4 * hf;
-            const f32x4 qa = *reinterpret_cast<const f32x4 *>(&q_lds[l32 * kLdsStride + col]);
-            const f32x4 qb = *reinterpret_cast<const f32x4 *>(&q_lds[(32 + l32) * kLdsStride + col]);
-            const f32x4 da = *reinterpret_cast<const f32x4 *>(&do_lds[l32 * kLdsStride + col]);
-            const f32x4 db = *reinterpret_cast<const f32x4 *>(&do_lds[(32 + l32) * kLdsStride + col]);
+            for (int j = 0; j < 8; ++j) {
+                const int col = 8 * j + 4 * hf;
+                const f32x4 qa = *reinterpret_cast<const f32x4 *>(&q_lds[(32 * qb + l32) * kLdsStride + col]);
+                const f32x4 da = *reinterpret_cast<const f32x4 *>(&do_lds[(32 * qb + l32) * kLdsStride + col]);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                s[0] = mfma32(qa[c], kr[j][c], s[0]);
-                s[1] = mfma32(qb[c], kr[j][c], s[1]);
-                dp[0] = mfma32(da[c], vr[j][c], dp[0]);
-                dp[1] = mfma32(db[c], vr[j][c], dp[1]);
+                for (int c = 0; c < 4; ++c) {
+                    s = mfma32(qa[c], kr[j][c], s);
+                    dp = mfma32(da[c], vr[j][c], dp);
+                }
             }
-        }
 
-        const bool diag = q0 < kw0 + 31;
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+            const bool diag = qh0 < kw0 + 31;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lse_lds[32 * qb + 8 * g + 4 * hf]);
@@ -165,24 +165,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int r = 4 * g + c;
-                    float p = fast_exp2(fmaf(s[qb][r], c2, -l4[c]));
-                    if (diag && q0 + 32 * qb + 8 * g + 4 * hf + c < my_k) p = 0.0f;
-                    s[qb][r] = p;                          // P
-                    dp[qb][r] = p * (dp[qb][r] - d4[c]);   // dS
+                    float p = fast_exp2(fmaf(s[r], c2, -l4[c]));
+                    if (diag && qh0 + 8 * g + 4 * hf + c < my_k) p = 0.0f;
+                    s[r] = p;                        // P
+                    dp[r] = p * (dp[r] - d4[c]);     // dS
                 }
             }
 
-        // Hand dS to the dq kernel: block (qt, key block kw0/32), [64 queries][32 keys].
-        float *dsb = a.ds + ds_block_offset(bh, a.nqt, qt, kw0 >> 5);
+            // Hand dS to the dq kernel: block (qt, key block kw0/32), [64 queries][32 keys].
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                dsb[(32 * qb + 8 * (r >> 2) + 4 * hf + (r & 3)) * 32 + l32] = dp[qb][r];
+            for (int r = 0; r < 16; ++r) dsb[(32 * qb + 8 * (r >> 2) + 4 * hf + (r & 3)) * 32 + l32] = dp[r];
 
-        // dV += P^T dO and dK += dS^T Q (keys x dims).
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+            // dV += P^T dO and dK += dS^T Q (keys x dims).
 #pragma unroll
             for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -192,11 +186,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams a) {
                     const float d1 = do_lds[row * kLdsStride + 32 + l32];
                     const float q0v = q_lds[row * kLdsStride + l32];
                     const float q1v = q_lds[row * kLdsStride + 32 + l32];
-                    acc_dv[0] = mfma32(s[qb][4 * g + c], d0, acc_dv[0]);
-                    acc_dv[1] = mfma32(s[qb][4 * g + c], d1, acc_dv[1]);
-                    acc_dk[0] = mfma32(dp[qb][4 * g + c], q0v, acc_dk[0]);
-                    acc_dk[1] = mfma32(dp[qb][4 * g + c], q1v, acc_dk[1]);
+                    acc_dv[0] = mfma32(s[4 * g + c], d0, acc_dv[0]);
+                    acc_dv[1] = mfma32(s[4 * g + c], d1, acc_dv[1]);
+                    acc_dk[0] = mfma32(dp[4 * g + c], q0v, acc_dk[0]);
+                    acc_dk[1] = mfma32(dp[4 * g + c], q1v, acc_dk[1]);
                 }
+        }
     }
 
     // Accumulator layout (keys x dims): lane -> dim 32*db + l32,
@@ -253,13 +248,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
             const int key = kt * kBwdBN + ld_row + 16 * i;
             kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
         }
-        // Tiles past this wave's diagonal and key blocks wholly past T were
-        // never written: read nothing from them.
-        const bool on = wave_on && kt * kBwdBN <= qw0 + 31;
+        // Key blocks past this wave's diagonal (all of dS zero there) or wholly
+        // past T are never written by the dk/dv kernel: read nothing from them.
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             const int kb32 = 2 * kt + kb;
-            const bool ok = on && 32 * kb32 < T;
+            const bool ok = wave_on && 32 * kb32 <= qw0 && 32 * kb32 < T;
 #pragma unroll
             for (int g = 0; g < 4; ++g)
                 dsn[kb][g] = ok ? *reinterpret_cast<const f32x4 *>(ds_row + kb32 * kDsBlock + 8 * g) : zero4();
