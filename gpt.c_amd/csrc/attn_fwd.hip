@@ -21,6 +21,7 @@ namespace gptc {
 
 constexpr int kFwdBM = 128;  // queries per workgroup
 constexpr int kFwdBN = 64;   // keys per LDS tile
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 
 template <bool VEC, bool PERM>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
@@ -127,31 +128,44 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
                 }
         }
 
-        float mt = -INFINITY;
+        // Row max of this tile: 4 independent chains, then the other wave half.
+        float mx[4];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int i = 0; i < 4; ++i) mx[i] = fmaxf(s[i >> 1][(i & 1) * 8], s[i >> 1][(i & 1) * 8 + 1]);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
-        mt = fmaxf(mt, other_half(mt));
-        const float m_new = fmaxf(m_run, mt * c2);
-        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = fast_exp2(m_run - m_use);
-        float ls = 0.0f;
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 2; r < 8; ++r) mx[i] = fmaxf(mx[i], s[i >> 1][(i & 1) * 8 + r]);
+        float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+        mt = fmaxf(mt, other_half(mt)) * c2;
+
+        // Lazy rescaling: the running max only moves when some row's max grows
+        // by more than 2^kRescaleLog2 (or on the first tile).  In between, the
+        // exponents are taken against a stale max, so p <= 2^kRescaleLog2,
+        // which fp32 holds exactly as well; the final y = acc / l is the same.
+        if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleLog2) != 0) {
+            const float m_new = fmaxf(m_run, mt);
+            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+            const float alpha = fast_exp2(m_run - m_use);
+            l_run *= alpha;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc_o[0][r] *= alpha;
+                acc_o[1][r] *= alpha;
+            }
+            m_run = m_new;
+        }
+        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float p = fast_exp2(fmaf(s[kb][r], c2, -m_use));
                 s[kb][r] = p;
-                ls += p;
+                ls[r & 3] += p;
             }
-        l_run = fmaf(l_run, alpha, ls);
-        m_run = m_new;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            acc_o[0][r] *= alpha;
-            acc_o[1][r] *= alpha;
-        }
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 
         // O^T (dims x queries) += V^T P^T; P^T register 4g+c is the B operand.
 #pragma unroll
