@@ -68,7 +68,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __shared__ __attribute__((aligned(16))) float dl_lds[kBwdBQ];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
+    // The wave index is made visibly uniform (an SGPR): branches on it are then
+    // scalar branches instead of exec-masked divergent regions around MFMAs.
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
     const int bh = blockIdx.x % a.bh_pad;
     if (bh >= a.B * a.H) return;
     // Low key blocks see the most queries: launch them first.
@@ -219,7 +222,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[kBwdBN * kLdsStride];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
+    // The wave index is made visibly uniform (an SGPR): branches on it are then
+    // scalar branches instead of exec-masked divergent regions around MFMAs.
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
     const int bh = blockIdx.x % a.bh_pad;
     if (bh >= a.B * a.H) return;
     const int qb = a.nqb - 1 - static_cast<int>(blockIdx.x / a.bh_pad);

@@ -29,7 +29,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
     __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, hf = lane >> 5, l32 = lane & 31;
+    // The wave index is made visibly uniform (an SGPR): branches on it are then
+    // scalar branches instead of exec-masked divergent regions around MFMAs.
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
 
     // Longest query blocks first; the (b, h) index runs fastest so that all
     // query blocks of one head share blockIdx % 8 and hence one XCD's L2.

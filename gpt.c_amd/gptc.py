@@ -144,8 +144,13 @@ def build():
     subprocess.run(["make", "-B", "-j8", "-C", HERE], check=True, stdout=subprocess.DEVNULL)
 
 
-def load(path=LIB_PATH):
-    """dlopen the library and attach signatures; raises if it is missing."""
+def load(path=None):
+    """dlopen the library and attach signatures; raises if it is missing.
+
+    The path defaults to the in-tree build, or $GPTC_LIB when set (to compare
+    two builds of the library side by side).
+    """
+    path = path or os.environ.get("GPTC_LIB") or LIB_PATH
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built: run __graft_entry__.build() (make -C gpt.c_amd)")
     lib = ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
