@@ -209,8 +209,10 @@ def main():
     xt = rt.from_numpy(x)
     dyt = rt.from_numpy(dy)
     mask = rt.from_numpy(np.tril(np.ones((T, T), np.float32)))
-    # Compact cache layout of the library's Attention(): cache[0] is the input itself.
-    caches = (gptc.TensorP * 4)(xt, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((B, H, T)))
+    # Compact cache layout of the library's Attention(): cache[0] is the input
+    # itself, cache[3] the 1-D backward state (probability blocks and maxima).
+    n_state = lib.gptc_attention_state_floats(B, T, C, H)
+    caches = (gptc.TensorP * 4)(xt, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((n_state,)))
     yt = rt.empty((B, T, C))
     dqkv = rt.empty((B, T, 3 * C))
     rt.sync()

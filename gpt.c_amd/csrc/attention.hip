@@ -5,6 +5,7 @@
 // kernels/src/core/Attention.c:40-41,75-76).
 #include <cmath>
 #include <cstdint>
+#include <initializer_list>
 #include "attn_kernels.hpp"
 #include "gpu_kernels.h"
 #include "hip_check.hpp"
@@ -24,6 +25,15 @@ struct Dims {
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int bh_padded(int bh) { return (bh + 7) / 8 * 8; }
+
+// The buffer-resource tile loads (FULL kernels) need D == kDPad and the rows
+// of one head, row stride st floats, to span fewer than 2^31 bytes.
+bool full_tiles(const Dims &d, std::initializer_list<uint32_t> strides) {
+    if (d.D != gptc::kDPad) return false;
+    for (uint32_t st : strides)
+        if ((static_cast<int64_t>(d.T - 1) * st + gptc::kDPad) * 4 >= (1LL << 31)) return false;
+    return true;
+}
 
 void check_head_size(const Dims &d) {
     CHECK_ERROR(d.H <= 0 || d.C % d.H != 0, "Expected C = %d to be divisible by n_heads = %d.", d.C, d.H);
@@ -56,10 +66,53 @@ bool is_bhtd(const tensor_t *t, const Dims &d) {
     return t->ndims == 4 && t->shape[0] == d.B && t->shape[1] == d.H && t->shape[2] == d.T && t->shape[3] == d.D;
 }
 
-// Floats of the compact state kept in cache[3] by the reference cache
-// layout: y copy (B*T*C), log-sum-exp (B*H*T), delta scratch (B*H*T).
-int64_t packed_state_len(const Dims &d) {
-    return static_cast<int64_t>(d.B) * d.T * d.C + 2LL * d.B * d.H * d.T;
+int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
+
+// Float offsets of the state that cache[3] carries from forward to backward,
+// each part 256-byte aligned:
+//   [y copy (B*T*C) | log-sum-exp (B*H*T)]   reference cache layout only
+//   delta (B*H*T)                            written by the backward
+//   m (B*H*nqt*T)                            per-tile row maxima of P'
+//   P' / dS blocks (bwd_ds_floats)           P' from forward, dS in backward
+struct StateLayout {
+    int64_t y, lse, delta, m, p, total;
+};
+
+StateLayout state_layout(const Dims &d, bool reference_layout) {
+    const int64_t btc = static_cast<int64_t>(d.B) * d.T * d.C;
+    const int64_t bht = static_cast<int64_t>(d.B) * d.H * d.T;
+    const int64_t nqt = (d.T + 63) / 64;
+    StateLayout s{};
+    int64_t off = 0;
+    if (reference_layout) {
+        s.y = off;
+        off += align64(btc);
+        s.lse = off;
+        off += align64(bht);
+    }
+    s.delta = off;
+    off += align64(bht);
+    s.m = off;
+    off += align64(bht * nqt);
+    s.p = off;
+    off += static_cast<int64_t>(gptc::bwd_ds_floats(d.B, d.H, d.T));
+    s.total = off;
+    CHECK_ERROR(s.total > INT32_MAX,
+                "Attention state of %lld floats for B=%d, T=%d, H=%d exceeds the int length of a tensor_t.",
+                (long long)s.total, d.B, d.T, d.H);
+    return s;
+}
+
+// Makes `t` a 1-D device tensor of exactly n floats (the backward state),
+// replacing its storage unless it already is one.
+void ensure_state_tensor(tensor_t *t, int64_t n) {
+    if (t->ndims == 1 && t->length == n) return;
+    free_cuda(t->t);
+    t->t = static_cast<float *>(alloc_cuda(static_cast<size_t>(n) * sizeof(float)));
+    t->ndims = 1;
+    t->length = static_cast<int>(n);
+    for (int i = 0; i < 8; i++) t->shape[i] = 0;
+    t->shape[0] = static_cast<int>(n);
 }
 
 // Events registered by gptc_set_kernel_events: [0,1] around the forward
@@ -112,36 +165,35 @@ extern "C" void attention_forward_cuda_kernel(const tensor_t *input, const tenso
     p.o = btc_view<HeadViewW>(output->t, d);
     const int64_t bht = static_cast<int64_t>(d.B) * d.H * d.T;
 
-    if (cache[0] == input || cache[0]->t == input->t) {
-        // Compact layout: the layer keeps the input itself.
+    const bool compact = cache[0] == input || cache[0]->t == input->t;
+    const StateLayout st = state_layout(d, !compact);
+    if (compact) {
+        // Compact layout: the layer keeps the input itself, a copy of y in
+        // cache[1], the log-sum-exp in cache[2] and the backward state in
+        // cache[3] (re-pointed here unless it already has the state's size).
         CHECK_ERROR(cache[1]->length != output->length, "Expected cache[1] of %d elements (copy of the output).",
                     output->length);
-        CHECK_ERROR(cache[2]->length < bht || cache[3]->length < bht,
-                    "Expected cache[2] and cache[3] of at least B*H*T = %lld elements.", (long long)bht);
+        CHECK_ERROR(cache[2]->length < bht, "Expected cache[2] of at least B*H*T = %lld elements.", (long long)bht);
+        ensure_state_tensor(cache[3], st.total);
         p.o2 = cache[1]->t;
         p.lse = cache[2]->t;
         p.qp = p.kp = p.vp = nullptr;
     } else {
         // Reference layout (gpt.c attention.c:105-120): permuted q, k, v go to
-        // cache[0..2]; cache[3] is re-pointed to the compact state.
+        // cache[0..2]; cache[3] is re-pointed from the (B, H, T, T) P to the
+        // compact state, which includes y and the log-sum-exp.
         for (int i = 0; i < 3; i++)
             CHECK_ERROR(!is_bhtd(cache[i], d), "Expected cache[%d] of shape (B, H, T, D) = (%d, %d, %d, %d).", i, d.B,
                         d.H, d.T, d.D);
-        const int64_t need = packed_state_len(d);
-        if (cache[3]->length != need || cache[3]->ndims != 1) {
-            free_cuda(cache[3]->t);
-            cache[3]->t = static_cast<float *>(alloc_cuda(static_cast<size_t>(need) * sizeof(float)));
-            cache[3]->ndims = 1;
-            cache[3]->length = static_cast<int>(need);
-            for (int i = 0; i < 8; i++) cache[3]->shape[i] = 0;
-            cache[3]->shape[0] = static_cast<int>(need);
-        }
-        p.o2 = cache[3]->t;
-        p.lse = cache[3]->t + static_cast<int64_t>(d.B) * d.T * d.C;
+        ensure_state_tensor(cache[3], st.total);
+        p.o2 = cache[3]->t + st.y;
+        p.lse = cache[3]->t + st.lse;
         p.qp = cache[0]->t;
         p.kp = cache[1]->t;
         p.vp = cache[2]->t;
     }
+    p.pm = cache[3]->t + st.m;
+    p.pp = cache[3]->t + st.p;
 
     p.B = d.B;
     p.H = d.H;
@@ -149,9 +201,11 @@ extern "C" void attention_forward_cuda_kernel(const tensor_t *input, const tenso
     p.D = d.D;
     p.scale_log2 = gptc::kLog2e / std::sqrt(static_cast<float>(d.D));
     p.nqb = (d.T + 127) / 128;
+    p.nqt = (d.T + 63) / 64;
     p.bh_pad = bh_padded(d.B * d.H);
     p.vec = (d.D % 4 == 0) && aligned16(input->t) && aligned16(output->t) && aligned16(p.o2) &&
             (!p.qp || (aligned16(p.qp) && aligned16(p.kp) && aligned16(p.vp)));
+    p.full = p.vec && full_tiles(d, {p.k.st, p.v.st});
     gptc::launch_attn_fwd(p, gptc_stream_checked(), g_have_events ? g_events : nullptr);
 }
 
@@ -180,30 +234,33 @@ extern "C" void attention_backward_cuda_kernel(const tensor_t *global_grad, tens
     const int64_t btc = static_cast<int64_t>(d.B) * d.T * d.C;
     const int64_t bht = static_cast<int64_t>(d.B) * d.H * d.T;
     const tensor_t *c0 = cache[0];
-    const float *state = nullptr;
-    if (c0->ndims == 3 && c0->shape[0] == d.B && c0->shape[1] == d.T && c0->shape[2] == 3 * d.C) {
+    const float *y_saved = nullptr;
+    const bool compact = c0->ndims == 3 && c0->shape[0] == d.B && c0->shape[1] == d.T && c0->shape[2] == 3 * d.C;
+    const StateLayout st = state_layout(d, !compact);
+    CHECK_ERROR(cache[3]->ndims != 1 || cache[3]->length != st.total,
+                "cache[3] does not hold the state written by attention_forward_cuda_kernel for this shape.");
+    if (compact) {
         CHECK_ERROR(cache[1]->length != btc, "Expected cache[1] of B*T*C = %lld elements.", (long long)btc);
-        CHECK_ERROR(cache[2]->length < bht || cache[3]->length < bht,
-                    "Expected cache[2] and cache[3] of at least B*H*T = %lld elements.", (long long)bht);
+        CHECK_ERROR(cache[2]->length < bht, "Expected cache[2] of at least B*H*T = %lld elements.", (long long)bht);
         qkv_views(c0->t, d, p.q, p.k, p.v);
-        p.o = btc_view<HeadView>(static_cast<const float *>(cache[1]->t), d);
+        y_saved = cache[1]->t;
         p.lse = cache[2]->t;
-        p.delta = cache[3]->t;
-        state = cache[1]->t;
     } else {
         for (int i = 0; i < 3; i++)
             CHECK_ERROR(!is_bhtd(cache[i], d), "Expected cache[%d] of shape (B, H, T, D) = (%d, %d, %d, %d).", i, d.B,
                         d.H, d.T, d.D);
-        CHECK_ERROR(cache[3]->ndims != 1 || cache[3]->length != packed_state_len(d),
-                    "cache[3] does not hold the state written by attention_forward_cuda_kernel for this shape.");
         p.q = bhtd_view(cache[0]->t, d);
         p.k = bhtd_view(cache[1]->t, d);
         p.v = bhtd_view(cache[2]->t, d);
-        p.o = btc_view<HeadView>(static_cast<const float *>(cache[3]->t), d);
-        p.lse = cache[3]->t + btc;
-        p.delta = cache[3]->t + btc + bht;
-        state = cache[3]->t;
+        y_saved = cache[3]->t + st.y;
+        p.lse = cache[3]->t + st.lse;
     }
+    p.o = btc_view<HeadView>(y_saved, d);
+    p.delta = cache[3]->t + st.delta;
+    p.pm = cache[3]->t + st.m;
+    // The backward consumes the state: dS overwrites P' (gpt.c's CPU backward
+    // likewise reuses its caches as scratch, kernels/src/cpu/Attention.c:198-201).
+    p.ds = cache[3]->t + st.p;
     p.dout = btc_view<HeadView>(static_cast<const float *>(global_grad->t), d);
     const uint32_t sb3 = static_cast<uint32_t>(d.T) * 3 * d.C, st3 = 3 * d.C;
     p.dq = HeadViewW{dout->t, sb3, st3, static_cast<uint32_t>(d.D)};
@@ -215,17 +272,20 @@ extern "C" void attention_backward_cuda_kernel(const tensor_t *global_grad, tens
     p.T = d.T;
     p.D = d.D;
     p.scale = 1.0f / std::sqrt(static_cast<float>(d.D));
-    p.scale_log2 = gptc::kLog2e * p.scale;
     p.nqb = (d.T + 127) / 128;
     p.nkb = (d.T + 127) / 128;
     p.nqt = (d.T + 63) / 64;
     p.bh_pad = bh_padded(d.B * d.H);
-    p.vec = (d.D % 4 == 0) && aligned16(p.q.p) && aligned16(p.k.p) && aligned16(p.v.p) && aligned16(state) &&
+    p.vec = (d.D % 4 == 0) && aligned16(p.q.p) && aligned16(p.k.p) && aligned16(p.v.p) && aligned16(y_saved) &&
             aligned16(global_grad->t) && aligned16(dout->t);
-
-    // dS scratch: stream-ordered, released right after the kernels that use it.
-    const size_t ds_floats = gptc::bwd_ds_floats(d.B, d.H, d.T);
-    p.ds = static_cast<float *>(alloc_cuda(ds_floats * sizeof(float)));
+    p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.dout.st});
     gptc::launch_attn_bwd(p, gptc_stream_checked(), g_have_events ? g_events + 2 : nullptr);
-    free_cuda(p.ds);
+}
+
+extern "C" long long gptc_attention_state_floats(int B, int T, int C, int n_heads) {
+    CHECK_ERROR(B < 0 || T < 0 || C < 0 || n_heads <= 0 || C % n_heads != 0,
+                "Expected B, T, C >= 0 and C divisible by n_heads > 0, but got B=%d, T=%d, C=%d, n_heads=%d.", B, T,
+                C, n_heads);
+    const Dims d{B, T, C, n_heads, C / n_heads};
+    return state_layout(d, false).total;
 }

@@ -1,23 +1,24 @@
-// Fused causal attention backward for gfx950 (FlashAttention-2 style: P is
-// rebuilt from the saved log-sum-exp, never stored).  Replaces gpt.c's
+// Fused causal attention backward for gfx950.  Like gpt.c's backward it
+// starts from the probabilities the forward kept (here the packed causal
+// blocks of P' with their per-tile maxima, rescaled by the saved
+// log-sum-exp; gpt.c keeps the full (B, H, T, T) P).  Replaces gpt.c's
 // unpermute / 4 batched SGEMMs / softmax backward / permute sequence
 // (kernels/src/cuda/Attention.cu:235-324; math of
 // kernels/src/cpu/Attention.c:169-301):
 //     dP = dO V^T,  dV = P^T dO,  dS = P o (dP - rowsum(dP o P)),
 //     dQ = dS K / sqrt(D),  dK = dS^T Q / sqrt(D),
-// using rowsum(dP o P) = rowsum(dO o O) =: delta.
+// using rowsum(dP o P) = rowsum(dO o O) =: delta.  These are the four
+// contractions of the reference; none is recomputed.
 //
 // Three kernels; every output element is written exactly once (no atomics,
 // no zeroed output needed, bit-for-bit deterministic):
 //   attn_bwd_delta_kernel  delta = rowsum(dO o O); streams dO and O once.
-//   attn_bwd_dkdv_kernel   key-parallel: per 32-key wave (K, V resident in
-//                          registers), over the query tiles: S, P, dP, dS,
-//                          dV += P^T dO, dK += dS^T Q.  It also stores the
-//                          causal tiles of dS, in the exact register layout
-//                          the dq kernel consumes them in.
-//   attn_bwd_dq_kernel     query-parallel: dQ^T += K^T dS^T, one
-//                          contraction per tile instead of recomputing S
-//                          and dP (two more contractions).
+//   attn_bwd_dkdv_kernel   key-parallel: per 32-key wave (V resident in
+//                          registers), over the query tiles: P from P',
+//                          dP, dS, dV += P^T dO, dK += dS^T Q.  dS
+//                          overwrites P' in place, in the exact register
+//                          layout the dq kernel consumes it in.
+//   attn_bwd_dq_kernel     query-parallel: dQ^T += K^T dS^T.
 // The accumulator of the score product is directly the operand of the
 // gradient products (see the layout note in attn_common.hpp).
 #include "attn_common.hpp"
@@ -59,13 +60,18 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) 
 }
 
 // ---- dK, dV (and the dS tiles) ----
-template <bool VEC>
+// FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the tile loads then
+// go through bounds-checked buffer resources (no branches, no row tests).
+template <bool VEC, bool FULL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_kernel(
     const BwdParams a) {
     __shared__ __attribute__((aligned(16))) float q_lds[kBwdBQ * kLdsStride];
     __shared__ __attribute__((aligned(16))) float do_lds[kBwdBQ * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float lse_lds[kBwdBQ];
-    __shared__ __attribute__((aligned(16))) float dl_lds[kBwdBQ];
+    // Per-query statistics of the tile, one entry per thread: [0, 128) the
+    // factors f of P = P' * f for the workgroup's two 64-key tiles
+    // ([key tile][query]), [128, 192) delta, [192, 256) unused.
+    __shared__ __attribute__((aligned(16))) float stat_lds[256];
+    const float *dl_lds = stat_lds + 2 * kBwdBQ;
 
     const int tid = threadIdx.x;
     // The wave index is made visibly uniform (an SGPR): branches on it are then
@@ -85,42 +91,80 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bool k_ok = my_k < T;
 
     const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
-    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
     const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
     const float *dOh = a.dout.p + b * a.dout.sb + h * a.dout.sh;
     const float *lse_h = a.lse + static_cast<uint32_t>(bh) * T;
     const float *dl_h = a.delta + static_cast<uint32_t>(bh) * T;
+    const float *pm_h = a.pm + static_cast<uint32_t>(bh) * a.nqt * T;
 
-    f32x4 kr[8], vr[8];
+    // V row of this lane's key, dims 8j + 4hf + c: B operand of dP = dO V^T.
+    f32x4 vr[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int dim = 8 * j + 4 * hf;
-        kr[j] = k_ok ? load4<VEC>(Kh + my_k * a.k.st, dim, D) : zero4();
-        vr[j] = k_ok ? load4<VEC>(Vh + my_k * a.v.st, dim, D) : zero4();
-    }
+    for (int j = 0; j < 8; ++j) vr[j] = k_ok ? load4<VEC>(Vh + my_k * a.v.st, 8 * j + 4 * hf, D) : zero4();
+    // Let these loads land here: a loop-invariant register with a load still
+    // counted as outstanding makes every use in the loop wait for all loads.
+    __builtin_amdgcn_s_waitcnt(0);
 
     const int qt0 = k_blk0 / kBwdBQ;
     const int n_qt = a.nqt;
     const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    const auto q_rows = head_rows(Qh, T, a.q.st);
+    const auto do_rows = head_rows(dOh, T, a.dout.st);
     f32x4 qpre[4], dpre[4];
-    float stat_pre = 0.0f;
+    float st0 = 0.0f, st1 = 0.0f;
+    bool st_ok = false;
     auto prefetch = [&](int qt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int q = qt * kBwdBQ + ld_row + 16 * i;
-            qpre[i] = (q < T) ? load4<VEC>(Qh + q * a.q.st, ld_col, D) : zero4();
-            dpre[i] = (q < T) ? load4<VEC>(dOh + q * a.dout.st, ld_col, D) : zero4();
+            if (FULL) {
+                qpre[i] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + ld_col);
+                dpre[i] = buffer_load4(do_rows, static_cast<uint32_t>(q) * a.dout.st + ld_col);
+            } else {
+                qpre[i] = (q < T) ? load4<VEC>(Qh + q * a.q.st, ld_col, D) : zero4();
+                dpre[i] = (q < T) ? load4<VEC>(dOh + q * a.dout.st, ld_col, D) : zero4();
+            }
         }
-        if (tid < 2 * kBwdBQ) {
-            const int q = qt * kBwdBQ + (tid & (kBwdBQ - 1));
-            // Rows past T get lse = +inf (P = 0) and delta = 0.
-            if (tid < kBwdBQ) stat_pre = (q < T) ? lse_h[q] * kLog2e : INFINITY;
-            else stat_pre = (q < T) ? dl_h[q] : 0.0f;
-        }
+        // Threads 0..127: m and lse of query (tid & 63) for key tile 2kb + tid/64;
+        // threads 128..191: delta.  Loads from clamped, always valid addresses;
+        // rows past T (and a key tile past T) get f = 0 and delta = 0 when the
+        // values are written to LDS.  Arithmetic or selects on them here would
+        // make the wave wait for all its outstanding loads at once.
+        const int q = qt * kBwdBQ + (tid & (kBwdBQ - 1));
+        const int qc = min(q, T - 1);
+        const bool is_m = tid < 2 * kBwdBQ;
+        const int kt = 2 * kb_idx + ((tid >> 6) & 1);
+        st_ok = q < T && (!is_m || kt < n_qt);
+        st0 = *(is_m ? pm_h + min(kt, n_qt - 1) * T + qc : dl_h + qc);
+        st1 = lse_h[qc];
     };
     if (qt0 < n_qt) prefetch(qt0);
 
-    const float c2 = a.scale_log2;
+    // P' of one 32-query half, loaded one half ahead of its use: register r
+    // holds query 8(r/4) + 4hf + r%4 of the half, key my_k (the accumulator
+    // layout of a queries x keys product).  A half is needed when some of
+    // its queries see some of this wave's keys and it starts before T.  The
+    // forward wrote every row of such a half (finite values; rows at or past
+    // T get f = 0), so the loads need no row check.
+    float pbuf[16];
+    auto half_needed = [&](int qt, int qb) {
+        const int qh0 = qt * kBwdBQ + 32 * qb;
+        return qh0 + 31 >= kw0 && kw0 < T && qh0 < T;
+    };
+    // This wave's half of block (qt, kw0/32): a uniform base (SGPRs) plus a
+    // lane offset, so that every row of the half is an immediate offset.
+    const uint32_t lane_off = 4 * hf * 32 + l32;
+    auto half_base = [&](int qt, int qb) {
+        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh, n_qt, qt, kw0 >> 5)) + 32 * qb * 32);
+    };
+    auto load_p = [&](int qt, int qb) {
+        if (!half_needed(qt, qb)) return;
+        const float *hb = half_base(qt, qb);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
+    };
+    if (qt0 < n_qt) load_p(qt0, 0);
+
     f32x16 acc_dk[2] = {zero16(), zero16()};
     f32x16 acc_dv[2] = {zero16(), zero16()};
 
@@ -132,52 +176,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             *reinterpret_cast<f32x4 *>(&q_lds[row * kLdsStride + ld_col]) = qpre[i];
             *reinterpret_cast<f32x4 *>(&do_lds[row * kLdsStride + ld_col]) = dpre[i];
         }
-        if (tid < kBwdBQ) lse_lds[tid] = stat_pre;
-        else if (tid < 2 * kBwdBQ) dl_lds[tid - kBwdBQ] = stat_pre;
+        // Unconditional, so that no exec-masked branch sits between the loads
+        // and their uses (branches make the wait counts conservative).
+        {
+            const float f = fast_exp2(st0 - st1 * kLog2e);
+            stat_lds[tid] = st_ok ? (tid < 2 * kBwdBQ ? f : st0) : 0.0f;
+        }
         __syncthreads();
-        if (qt + 1 < n_qt) prefetch(qt + 1);
 
-        const int q0 = qt * kBwdBQ;
-        float *dsb = a.ds + ds_block_offset(bh, a.nqt, qt, kw0 >> 5);
-        // The tile's two 32-query halves one after the other: one S and one dP
-        // accumulator live at a time, which keeps the wave within the register
-        // budget of two waves per SIMD.
+        const float *f_w = stat_lds + (w >> 1) * kBwdBQ;  // this wave's key tile
+        // The tile's two 32-query halves one after the other: one P and one dP
+        // block live at a time, which keeps the wave within the register budget
+        // of two waves per SIMD.
         for (int qb = 0; qb < 2; ++qb) {
-            const int qh0 = q0 + 32 * qb;
-            if (qh0 + 31 < kw0 || kw0 >= T) continue;  // all queries precede all keys
-
-            // S and dP (queries x keys) for this 32-query half.
-            f32x16 s = zero16(), dp = zero16();
+            const bool need = half_needed(qt, qb);
+            f32x16 s, dp = zero16();
+            if (need) {
+                // dP (queries x keys) for this 32-query half.
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int col = 8 * j + 4 * hf;
-                const f32x4 qa = *reinterpret_cast<const f32x4 *>(&q_lds[(32 * qb + l32) * kLdsStride + col]);
-                const f32x4 da = *reinterpret_cast<const f32x4 *>(&do_lds[(32 * qb + l32) * kLdsStride + col]);
+                for (int j = 0; j < 8; ++j) {
+                    const f32x4 da = *reinterpret_cast<const f32x4 *>(
+                        &do_lds[(32 * qb + l32) * kLdsStride + 8 * j + 4 * hf]);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    s = mfma32(qa[c], kr[j][c], s);
-                    dp = mfma32(da[c], vr[j][c], dp);
+                    for (int c = 0; c < 4; ++c) dp = mfma32(da[c], vr[j][c], dp);
+                }
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 f4 = *reinterpret_cast<const f32x4 *>(&f_w[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) s[4 * g + c] = pbuf[4 * g + c] * f4[c];  // P
                 }
             }
+            // The next half's P' (its registers are free now).
+            if (qb == 0) {
+                load_p(qt, 1);
+                // Issued after this half's P' is consumed, so that waiting for
+                // that P' never waits for these loads.
+                if (qt + 1 < n_qt) prefetch(qt + 1);
+            } else if (qt + 1 < n_qt) {
+                load_p(qt + 1, 0);
+            }
+            if (!need) continue;
 
-            const bool diag = qh0 < kw0 + 31;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lse_lds[32 * qb + 8 * g + 4 * hf]);
                 const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&dl_lds[32 * qb + 8 * g + 4 * hf]);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int r = 4 * g + c;
-                    float p = fast_exp2(fmaf(s[r], c2, -l4[c]));
-                    if (diag && qh0 + 8 * g + 4 * hf + c < my_k) p = 0.0f;
-                    s[r] = p;                        // P
-                    dp[r] = p * (dp[r] - d4[c]);     // dS
-                }
+                for (int c = 0; c < 4; ++c) dp[4 * g + c] = s[4 * g + c] * (dp[4 * g + c] - d4[c]);  // dS
             }
 
-            // Hand dS to the dq kernel: block (qt, key block kw0/32), [64 queries][32 keys].
+            // dS replaces P' in place: block (qt, key block kw0/32), [64 queries][32 keys].
+            float *hb = half_base(qt, qb);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) dsb[(32 * qb + 8 * (r >> 2) + 4 * hf + (r & 3)) * 32 + l32] = dp[r];
+            for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
 
             // dV += P^T dO and dK += dS^T Q (keys x dims).
 #pragma unroll
@@ -217,7 +268,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // ---- dQ = dS K / sqrt(D) from the stored dS tiles ----
-template <bool VEC>
+template <bool VEC, bool FULL>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[kBwdBN * kLdsStride];
 
@@ -238,10 +289,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
     const bool wave_on = qw0 < T;
 
     const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+    const auto k_rows = head_rows(Kh, T, a.k.st);
     // This lane's dS row (query my_q) inside its 64-query tile: key block kb32
-    // starts kb32 * 2048 floats further; keys 8g + 4hf + c come as float4 g.
+    // starts kb32 * 2048 floats after the (uniform) tile base; keys
+    // 8g + 4hf + c come as float4 g.
     const int qt = qw0 >> 6;
-    const float *ds_row = a.ds + ds_block_offset(bh, a.nqt, qt, 0) + ((qw0 & 32) + l32) * 32 + 4 * hf;
+    const float *ds_tile = a.ds + ds_block_offset(bh, a.nqt, qt, 0);
+    const uint32_t row_off = ((qw0 & 32) + l32) * 32 + 4 * hf;
 
     const int kv_end = min(T, q_blk0 + kBwdBM);
     const int n_tiles = (kv_end + kBwdBN - 1) / kBwdBN;
@@ -252,7 +306,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int key = kt * kBwdBN + ld_row + 16 * i;
-            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
+            if (FULL)
+                kpre[i] = buffer_load4(k_rows, static_cast<uint32_t>(key) * a.k.st + ld_col);
+            else
+                kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
         }
         // Key blocks past this wave's diagonal (all of dS zero there) or wholly
         // past T are never written by the dk/dv kernel: read nothing from them.
@@ -262,7 +319,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
             const bool ok = wave_on && 32 * kb32 <= qw0 && 32 * kb32 < T;
 #pragma unroll
             for (int g = 0; g < 4; ++g)
-                dsn[kb][g] = ok ? *reinterpret_cast<const f32x4 *>(ds_row + kb32 * kDsBlock + 8 * g) : zero4();
+                dsn[kb][g] = ok ? *reinterpret_cast<const f32x4 *>(ds_tile + kb32 * kDsBlock + row_off + 8 * g)
+                                : zero4();
         }
     };
     prefetch(0);
@@ -329,19 +387,23 @@ void launch_attn_bwd(const BwdParams &p, hipStream_t stream, const hipEvent_t *e
         hipCheck(hipEventRecord(ev[1], stream));
         hipCheck(hipEventRecord(ev[2], stream));
     }
-    if (p.vec)
-        attn_bwd_dkdv_kernel<true><<<grid_k, block, 0, stream>>>(p);
+    if (p.full)
+        attn_bwd_dkdv_kernel<true, true><<<grid_k, block, 0, stream>>>(p);
+    else if (p.vec)
+        attn_bwd_dkdv_kernel<true, false><<<grid_k, block, 0, stream>>>(p);
     else
-        attn_bwd_dkdv_kernel<false><<<grid_k, block, 0, stream>>>(p);
+        attn_bwd_dkdv_kernel<false, false><<<grid_k, block, 0, stream>>>(p);
     hipCheck(hipGetLastError());
     if (ev) {
         hipCheck(hipEventRecord(ev[3], stream));
         hipCheck(hipEventRecord(ev[4], stream));
     }
-    if (p.vec)
-        attn_bwd_dq_kernel<true><<<grid_q, block, 0, stream>>>(p);
+    if (p.full)
+        attn_bwd_dq_kernel<true, true><<<grid_q, block, 0, stream>>>(p);
+    else if (p.vec)
+        attn_bwd_dq_kernel<true, false><<<grid_q, block, 0, stream>>>(p);
     else
-        attn_bwd_dq_kernel<false><<<grid_q, block, 0, stream>>>(p);
+        attn_bwd_dq_kernel<false, false><<<grid_q, block, 0, stream>>>(p);
     hipCheck(hipGetLastError());
     if (ev) hipCheck(hipEventRecord(ev[5], stream));
 }

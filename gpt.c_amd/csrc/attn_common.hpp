@@ -67,6 +67,37 @@ __device__ __forceinline__ f32x4 load4(const float *row, int dim, int D) {
     return v;
 }
 
+// Raw buffer resources (dword 3 of a gfx9 buffer descriptor): loads through
+// them are bounds-checked by the hardware against num_records and return
+// zeros past it, so tile loads need neither branches nor row tests.
+constexpr int kBufferConfig = 0x00020000;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// A wave-uniform value the compiler cannot prove uniform (it would otherwise
+// keep it in VGPRs, and a buffer resource in VGPRs costs a waterfall loop
+// around every load).
+__device__ __forceinline__ uint32_t uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+template <typename T>
+__device__ __forceinline__ T *uniform(T *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = uniform(static_cast<uint32_t>(v)), hi = uniform(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<T *>((hi << 32) | lo);
+}
+
+// Rows [0, rows) of one head (row t at t * st floats, kDPad floats used):
+// a row at or past `rows` reads as zeros.  The host guarantees that the byte
+// size fits in 31 bits before it selects the kernels that use this.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rows(const float *base, int rows, uint32_t st) {
+    const int bytes = rows > 0 ? static_cast<int>(uniform(((rows - 1) * st + kDPad) * 4u)) : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(uniform(base)), 0, bytes, kBufferConfig);
+}
+
+// Four floats at float offset `off` of a buffer resource.
+__device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0));
+}
+
 template <bool VEC>
 __device__ __forceinline__ void store4(float *row, int dim, int D, f32x4 v) {
     if (VEC) {

@@ -1,6 +1,8 @@
 // Fused causal attention forward for gfx950: S = QK^T / sqrt(D), causal
-// mask, online softmax and O = PV in one pass; writes O and the row
-// log-sum-exp.  Replaces the permute / batched SGEMM / mask / softmax /
+// mask, online softmax and O = PV in one pass; writes O, the row
+// log-sum-exp and, for the backward, the probabilities P' against the
+// running maximum with that maximum m per 64-key tile (the layout is
+// described in attn_kernels.hpp).  Replaces the permute / batched SGEMM / mask / softmax /
 // batched SGEMM / unpermute sequence of gpt.c
 // (kernels/src/cuda/Attention.cu:170-232; math of
 // kernels/src/cpu/Attention.c:46-167).
@@ -23,7 +25,9 @@ constexpr int kFwdBM = 128;  // queries per workgroup
 constexpr int kFwdBN = 64;   // keys per LDS tile
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 
-template <bool VEC, bool PERM>
+// FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the K/V tile loads
+// then go through bounds-checked buffer resources (no branches, no row tests).
+template <bool VEC, bool FULL, bool PERM>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
     __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
@@ -66,13 +70,20 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
 
     // Cooperative tile load: thread covers rows (tid>>4) + 16i, dims 4*(tid&15).
     const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    const auto k_rows = head_rows(Kh, T, a.k.st);
+    const auto v_rows = head_rows(Vh, T, a.v.st);
     f32x4 kpre[4], vpre[4];
     auto prefetch = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int key = kt * kFwdBN + ld_row + 16 * i;
-            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
-            vpre[i] = (key < T) ? load4<VEC>(Vh + key * a.v.st, ld_col, D) : zero4();
+            if (FULL) {
+                kpre[i] = buffer_load4(k_rows, static_cast<uint32_t>(key) * a.k.st + ld_col);
+                vpre[i] = buffer_load4(v_rows, static_cast<uint32_t>(key) * a.v.st + ld_col);
+            } else {
+                kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
+                vpre[i] = (key < T) ? load4<VEC>(Vh + key * a.v.st, ld_col, D) : zero4();
+            }
         }
     };
     prefetch(0);
@@ -170,6 +181,22 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
             }
         l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 
+        // Hand P' = p and m_use to the backward: this lane's query row of the
+        // packed blocks (qt, 2kt) and (qt, 2kt + 1), keys 8g + 4hf .. 8g + 4hf + 3.
+        // kt <= qt here, so both blocks exist; masked keys hold exact zeros.
+        {
+            float *pblk = a.pp + ds_block_offset(bh, a.nqt, qw0 >> 6, 2 * kt);  // uniform
+            const uint32_t prow = ((qw0 & 32) + l32) * 32 + 4 * hf;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 v = {s[kb][4 * g], s[kb][4 * g + 1], s[kb][4 * g + 2], s[kb][4 * g + 3]};
+                    *reinterpret_cast<f32x4 *>(pblk + kb * kDsBlock + prow + 8 * g) = v;
+                }
+            if (hf == 0 && my_q < T) a.pm[(static_cast<uint32_t>(bh) * a.nqt + kt) * T + my_q] = m_use;
+        }
+
         // O^T (dims x queries) += V^T P^T; P^T register 4g+c is the B operand.
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -209,14 +236,19 @@ void launch_attn_fwd(const FwdParams &p, hipStream_t stream, const hipEvent_t *e
     const dim3 grid(p.nqb * p.bh_pad), block(256);
     const bool vec = p.vec;
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
-    if (vec && p.qp)
-        attn_fwd_kernel<true, true><<<grid, block, 0, stream>>>(p);
+    const bool perm = p.qp != nullptr;
+    if (p.full && perm)
+        attn_fwd_kernel<true, true, true><<<grid, block, 0, stream>>>(p);
+    else if (p.full)
+        attn_fwd_kernel<true, true, false><<<grid, block, 0, stream>>>(p);
+    else if (vec && perm)
+        attn_fwd_kernel<true, false, true><<<grid, block, 0, stream>>>(p);
     else if (vec)
-        attn_fwd_kernel<true, false><<<grid, block, 0, stream>>>(p);
-    else if (p.qp)
-        attn_fwd_kernel<false, true><<<grid, block, 0, stream>>>(p);
+        attn_fwd_kernel<true, false, false><<<grid, block, 0, stream>>>(p);
+    else if (perm)
+        attn_fwd_kernel<false, false, true><<<grid, block, 0, stream>>>(p);
     else
-        attn_fwd_kernel<false, false><<<grid, block, 0, stream>>>(p);
+        attn_fwd_kernel<false, false, false><<<grid, block, 0, stream>>>(p);
     hipCheck(hipGetLastError());
     if (ev) hipCheck(hipEventRecord(ev[1], stream));
 }

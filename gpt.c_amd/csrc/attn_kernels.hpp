@@ -7,38 +7,14 @@
 
 namespace gptc {
 
-struct FwdParams {
-    HeadView q, k, v;     // inputs
-    HeadViewW o;          // y (B, T, C)
-    float *o2;            // optional copy of y, same strides as o (nullptr: none)
-    float *lse;           // (B, H, T) natural-log row log-sum-exp
-    float *qp, *kp, *vp;  // optional permuted copies (B, H, T, D) (nullptr: none)
-    int B, H, T, D;
-    float scale_log2;     // log2(e) / sqrt(D)
-    int nqb;              // ceil(T / 128)
-    int bh_pad;           // B*H rounded up to a multiple of 8
-    bool vec;             // D % 4 == 0 and every row 16-byte aligned
-};
-
-struct BwdParams {
-    HeadView q, k, v;     // saved inputs
-    HeadView o;           // saved y
-    HeadView dout;        // upstream gradient dy (B, T, C)
-    const float *lse;     // (B, H, T)
-    float *delta;         // (B, H, T) rowsum(dy * y), written by the delta kernel
-    float *ds;            // dS scratch, bwd_ds_floats(B, H, T) floats (packed causal tiles)
-    HeadViewW dq, dk, dv; // slices of dqkv (B, T, 3C)
-    int B, H, T, D;
-    float scale_log2;     // log2(e) / sqrt(D)
-    float scale;          // 1 / sqrt(D)
-    int nqb;              // ceil(T / 128) query blocks (dq kernel)
-    int nkb;              // ceil(T / 128) key blocks (dk/dv kernel)
-    int nqt;              // ceil(T / 64) query tiles of the dS store
-    int bh_pad;
-    bool vec;
-};
-
-// Stored dS: per (b, h), for each 64-query tile qt the 32-key blocks
+// The forward hands the backward the softmax probabilities it computed, so
+// that the backward needs no S = QK^T recomputation.  It stores them as
+//     P'[q][k] = exp2(S[q][k] * log2(e)/sqrt(D) - m[q][kt])
+// where m[q][kt] is the running row maximum (log2 units) that the forward
+// used for 64-key tile kt; the backward recovers
+//     P[q][k] = P'[q][k] * exp2(m[q][kt] - lse[q] * log2(e)).
+// P' and, in the backward, dS (which overwrites P' in place) share one packed
+// layout: per (b, h), for each 64-query tile qt the 32-key blocks
 // kb32 = 0 .. 2qt+1 (all that the causal rule leaves non-zero) follow one
 // another; block (qt, kb32) is a row-major [64 queries][32 keys] array.
 constexpr int kDsBlock = 64 * 32;
@@ -47,7 +23,44 @@ __host__ __device__ inline size_t ds_block_offset(int bh, int nqt, int qt, int k
     return (static_cast<size_t>(bh) * nqt * (nqt + 1) + static_cast<size_t>(qt) * (qt + 1) + kb32) * kDsBlock;
 }
 
+// Floats of the packed P' / dS blocks for a (B, H, T) problem.
 size_t bwd_ds_floats(int B, int H, int T);
+
+struct FwdParams {
+    HeadView q, k, v;     // inputs
+    HeadViewW o;          // y (B, T, C)
+    float *o2;            // optional copy of y, same strides as o (nullptr: none)
+    float *lse;           // (B, H, T) natural-log row log-sum-exp
+    float *qp, *kp, *vp;  // optional permuted copies (B, H, T, D) (nullptr: none)
+    float *pp;            // P' blocks, bwd_ds_floats(B, H, T) floats
+    float *pm;            // m, (B, H, nqt, T): m of query q for key tile kt at (bh*nqt + kt)*T + q
+    int B, H, T, D;
+    float scale_log2;     // log2(e) / sqrt(D)
+    int nqb;              // ceil(T / 128)
+    int nqt;              // ceil(T / 64)
+    int bh_pad;           // B*H rounded up to a multiple of 8
+    bool vec;             // D % 4 == 0 and every row 16-byte aligned
+    bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
+};
+
+struct BwdParams {
+    HeadView q, k, v;     // saved inputs
+    HeadView o;           // saved y
+    HeadView dout;        // upstream gradient dy (B, T, C)
+    const float *lse;     // (B, H, T)
+    const float *pm;      // m saved by the forward, (B, H, nqt, T)
+    float *delta;         // (B, H, T) rowsum(dy * y), written by the delta kernel
+    float *ds;            // in: P' from the forward; out: dS (same packed blocks)
+    HeadViewW dq, dk, dv; // slices of dqkv (B, T, 3C)
+    int B, H, T, D;
+    float scale;          // 1 / sqrt(D)
+    int nqb;              // ceil(T / 128) query blocks (dq kernel)
+    int nkb;              // ceil(T / 128) key blocks (dk/dv kernel)
+    int nqt;              // ceil(T / 64) query tiles of the P' / dS blocks
+    int bh_pad;
+    bool vec;
+    bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
+};
 
 // ev: optional events recorded on `stream` around each kernel launch
 // (forward: ev[0], ev[1]; backward: ev[0..1] around the delta kernel,

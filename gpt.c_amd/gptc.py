@@ -125,6 +125,7 @@ SIGNATURES = {
     "attention_backward_cuda_kernel": (None, [TensorP, ctypes.POINTER(TensorP), _ci, TensorP]),
     "gptc_stream": (_vp, []),
     "gptc_set_kernel_events": (None, [ctypes.POINTER(_vp), _ci]),
+    "gptc_attention_state_floats": (ctypes.c_longlong, [_ci, _ci, _ci, _ci]),
     # rand.h
     "manual_seed": (None, [_vp, ctypes.c_uint]),
     "randint32": (ctypes.c_uint, [_vp]),

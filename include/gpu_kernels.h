@@ -50,21 +50,29 @@ void copy_tensor_data_cuda(tensor_t *dst, const tensor_t *src);
  *          - compact (this library's attention.c): cache[0] IS the input
  *            tensor (ownership passed to the layer), cache[1] (B, T, C)
  *            receives a copy of the output, cache[2] (B, H, T) receives the
- *            row log-sum-exp, cache[3] (B, H, T) is backward scratch;
+ *            row log-sum-exp, cache[3] receives the backward state: the
+ *            causal blocks of the probabilities (about B*H*T*T/2 floats)
+ *            and their per-tile row maxima.  A cache[3] that is not a 1-D
+ *            tensor of gptc_attention_state_floats() floats is re-pointed
+ *            to one (stream-ordered free + alloc);
  *          - reference (gpt.c's unchanged attention.c:105-120): cache[0..2]
  *            (B, H, T, D) receive the permuted q, k, v exactly as gpt.c's
  *            CPU kernel writes them; cache[3], allocated (B, H, T, T), is
- *            re-pointed to a compact buffer holding the output copy, the
- *            log-sum-exp and backward scratch (the B*H*T*T probability
- *            matrix is never formed).
- *   Supported head sizes: D <= 64 (D = C / n_heads); T <= 65536.
+ *            re-pointed to a 1-D buffer holding the output copy, the
+ *            log-sum-exp and the backward state (about half the size of
+ *            the B*H*T*T probability matrix gpt.c keeps there).
+ *   Supported head sizes: D <= 64 (D = C / n_heads).  The state must fit
+ *   the int length of a tensor_t (checked, fatal otherwise).
  *
  * attention_backward_cuda_kernel(global_grad, cache, n_heads, dout)
  *   global_grad (B, T, C) upstream gradient (may be clobbered by the caller
  *   afterwards), cache as left by the forward, dout (B, T, 3C) receives
  *   dq | dk | dv.  Every element of dout is written (no accumulation), so
  *   dout need not be zeroed; a zeroed dout (gpt.c attention.c:142-143)
- *   gives the same result.
+ *   gives the same result.  The backward consumes cache[3] (its dS
+ *   overwrites the stored probabilities), as gpt.c's backward, which
+ *   frees the cache right after (attention.c:147-155), permits; a second
+ *   backward needs a new forward.  It allocates nothing.
  */
 void attention_forward_cuda_kernel(
     const tensor_t *input,
@@ -91,9 +99,14 @@ void attention_backward_cuda_kernel(
  * [0,1] the forward kernel, then the backward's [2,3] delta, [4,5] dk/dv
  * and [6,7] dq kernels.  They stay registered until the next call;
  * events == NULL stops the recording.  For per-kernel timing.
+ *
+ * gptc_attention_state_floats(B, T, C, n_heads): floats of the 1-D cache[3]
+ * that the compact layout's forward expects (and otherwise re-points), so
+ * that a layer can allocate it once at the right size.
  */
 void *gptc_stream(void);
 void gptc_set_kernel_events(void **events, int n);
+long long gptc_attention_state_floats(int B, int T, int C, int n_heads);
 
 #ifdef __cplusplus
 }
