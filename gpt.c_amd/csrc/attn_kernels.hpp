@@ -26,6 +26,8 @@ __host__ __device__ inline size_t ds_block_offset(int bh, int nqt, int qt, int k
 // Floats of the packed P' / dS blocks for a (B, H, T) problem.
 size_t bwd_ds_floats(int B, int H, int T);
 
+constexpr int kDqRounds = 4;  // co-resident dispatch rounds the dq order balances
+
 struct FwdParams {
     HeadView q, k, v;     // inputs
     HeadViewW o;          // y (B, T, C)
@@ -60,6 +62,8 @@ struct BwdParams {
     int bh_pad;
     bool vec;
     bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
+    int dq_cus;           // CUs per XCD the dq grid order is laid out for (0: plain order)
+    int dq_rot[kDqRounds];  // CU-index rotation of each co-resident dq dispatch round
 };
 
 // ev: optional events recorded on `stream` around each kernel launch
