@@ -25,11 +25,6 @@
 #include "attn_kernels.hpp"
 #include "hip_check.hpp"
 
-#include <algorithm>
-#include <array>
-#include <cstdint>
-#include <map>
-
 namespace gptc {
 
 constexpr int kBwdBK = 128;  // keys per dk/dv workgroup (32 per wave)
@@ -282,22 +277,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
     // scalar branches instead of exec-masked divergent regions around MFMAs.
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
-    // XCD- and CU-aware order.  Workgroup i of XCD x (blockIdx = 8i + x)
-    // lands on that XCD's CU i % cus in dispatch round i / cus, and all the
-    // rounds that fit stay resident together.  Position pos enumerates query
-    // blocks longest first (head index fastest, so every block of a head is on
-    // one XCD and shares its L2); rotating each round's CU index pairs long
-    // blocks with short ones on every CU.  pos is a permutation of i.
-    const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
-    const int nbh_x = a.bh_pad >> 3;
-    int pos = i;
-    if (a.dq_cus > 0) {
-        const int r = i / a.dq_cus, u = i - r * a.dq_cus;
-        if (r < kDqRounds && (r + 1) * a.dq_cus <= a.nqb * nbh_x) pos = r * a.dq_cus + (u + a.dq_rot[r]) % a.dq_cus;
-    }
-    const int qb = a.nqb - 1 - pos / nbh_x;
-    const int bh = x + 8 * (pos - (pos / nbh_x) * nbh_x);
+    // Query blocks in the XCD- and CU-aware order of grid_order.hpp.
+    int blk, bh;
+    grid_position(a.dq_order, a.nqb, a.bh_pad, blk, bh);
     if (bh >= a.B * a.H) return;
+    const int qb = a.nqb - 1 - blk;
     const int b = bh / a.H, h = bh - b * a.H;
     const int T = a.T, D = a.D;
 
@@ -391,69 +375,14 @@ size_t bwd_ds_floats(int B, int H, int T) {
     return static_cast<size_t>(B) * H * nqt * (nqt + 1) * kDsBlock;
 }
 
-namespace {
-
-constexpr int kXcds = 8;  // XCDs of an MI355X; workgroup i runs on XCD i % 8
-
-// Chooses the dq grid order (see attn_bwd_dq_kernel): the CU-index rotations of
-// the co-resident dispatch rounds that minimise the largest per-CU sum of
-// query-block lengths (ties: the largest smallest sum).  Cached per shape.
-template <typename Kernel>
-void choose_dq_order(BwdParams &p, Kernel kernel) {
-    p.dq_cus = 0;
-    for (int r = 0; r < kDqRounds; ++r) p.dq_rot[r] = 0;
-    int dev = 0, cus_total = 0, per_cu = 0;
-    hipCheck(hipGetDevice(&dev));
-    hipCheck(hipDeviceGetAttribute(&cus_total, hipDeviceAttributeMultiprocessorCount, dev));
-    hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0));
-    if (cus_total % kXcds != 0 || per_cu < 2) return;
-    const int cus = cus_total / kXcds, nbh_x = p.bh_pad / kXcds, M = p.nqb * nbh_x;
-    const int rounds = std::min(per_cu, kDqRounds);
-
-    static std::map<std::array<int, 4>, std::array<int, kDqRounds>> cache;
-    const std::array<int, 4> key{p.nqb, nbh_x, cus, rounds};
-    auto it = cache.find(key);
-    if (it == cache.end()) {
-        auto len = [&](int pos) { return pos < M ? p.nqb - pos / nbh_x : 0; };
-        std::array<int, kDqRounds> rot{}, best{};
-        int best_max = INT32_MAX, best_min = -1;
-        long combos = 1;
-        for (int r = 1; r < rounds; ++r) combos *= cus;
-        for (long c = 0; c < combos; ++c) {
-            long v = c;
-            for (int r = 1; r < rounds; ++r, v /= cus) rot[r] = static_cast<int>(v % cus);
-            int mx = 0, mn = INT32_MAX;
-            for (int u = 0; u < cus; ++u) {
-                int load = 0;
-                for (int r = 0; r < rounds; ++r) {
-                    const bool full = (r + 1) * cus <= M;
-                    load += len(r * cus + (full ? (u + rot[r]) % cus : u));
-                }
-                mx = std::max(mx, load);
-                mn = std::min(mn, load);
-            }
-            if (mx < best_max || (mx == best_max && mn > best_min)) {
-                best_max = mx;
-                best_min = mn;
-                best = rot;
-            }
-        }
-        it = cache.emplace(key, best).first;
-    }
-    p.dq_cus = cus;
-    for (int r = 0; r < kDqRounds; ++r) p.dq_rot[r] = it->second[r];
-}
-
-}  // namespace
-
 void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     BwdParams p = p_in;
     if (p.full)
-        choose_dq_order(p, attn_bwd_dq_kernel<true, true>);
+        p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<true, true>);
     else if (p.vec)
-        choose_dq_order(p, attn_bwd_dq_kernel<true, false>);
+        p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<true, false>);
     else
-        choose_dq_order(p, attn_bwd_dq_kernel<false, false>);
+        p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<false, false>);
     const dim3 block(256);
     const int rows = p.B * p.T * p.H;
     const dim3 grid_d((rows + 15) / 16), grid_k(p.nkb * p.bh_pad), grid_q(p.nqb * p.bh_pad);

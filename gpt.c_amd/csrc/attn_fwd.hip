@@ -28,7 +28,7 @@ constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 // FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the K/V tile loads
 // then go through bounds-checked buffer resources (no branches, no row tests).
 template <bool VEC, bool FULL, bool PERM>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_fwd_kernel(const FwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
     __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
 
@@ -38,11 +38,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
 
-    // Longest query blocks first; the (b, h) index runs fastest so that all
-    // query blocks of one head share blockIdx % 8 and hence one XCD's L2.
-    const int bh = blockIdx.x % a.bh_pad;
+    // Query blocks in the XCD- and CU-aware order of grid_order.hpp (three
+    // workgroups per CU, the whole C2 grid resident at once).
+    int blk, bh;
+    grid_position(a.order, a.nqb, a.bh_pad, blk, bh);
     if (bh >= a.B * a.H) return;
-    const int qb = a.nqb - 1 - static_cast<int>(blockIdx.x / a.bh_pad);
+    const int qb = a.nqb - 1 - blk;
     const int b = bh / a.H, h = bh - b * a.H;
     const int T = a.T, D = a.D;
 
@@ -232,11 +233,24 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams a) {
     if (hf == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(l_tot)) * kLn2;
 }
 
-void launch_attn_fwd(const FwdParams &p, hipStream_t stream, const hipEvent_t *ev) {
+void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
+    FwdParams p = p_in;
+    const bool perm = p.qp != nullptr;
+    if (p.full && perm)
+        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, true, true>);
+    else if (p.full)
+        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, true, false>);
+    else if (p.vec && perm)
+        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, false, true>);
+    else if (p.vec)
+        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, false, false>);
+    else if (perm)
+        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<false, false, true>);
+    else
+        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<false, false, false>);
     const dim3 grid(p.nqb * p.bh_pad), block(256);
     const bool vec = p.vec;
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
-    const bool perm = p.qp != nullptr;
     if (p.full && perm)
         attn_fwd_kernel<true, true, true><<<grid, block, 0, stream>>>(p);
     else if (p.full)

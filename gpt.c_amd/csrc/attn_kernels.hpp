@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <cstddef>
 #include "attn_common.hpp"
+#include "grid_order.hpp"
 
 namespace gptc {
 
@@ -26,8 +27,6 @@ __host__ __device__ inline size_t ds_block_offset(int bh, int nqt, int qt, int k
 // Floats of the packed P' / dS blocks for a (B, H, T) problem.
 size_t bwd_ds_floats(int B, int H, int T);
 
-constexpr int kDqRounds = 4;  // co-resident dispatch rounds the dq order balances
-
 struct FwdParams {
     HeadView q, k, v;     // inputs
     HeadViewW o;          // y (B, T, C)
@@ -43,6 +42,7 @@ struct FwdParams {
     int bh_pad;           // B*H rounded up to a multiple of 8
     bool vec;             // D % 4 == 0 and every row 16-byte aligned
     bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
+    GridOrder order;      // grid order (set by launch_attn_fwd)
 };
 
 struct BwdParams {
@@ -62,8 +62,7 @@ struct BwdParams {
     int bh_pad;
     bool vec;
     bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
-    int dq_cus;           // CUs per XCD the dq grid order is laid out for (0: plain order)
-    int dq_rot[kDqRounds];  // CU-index rotation of each co-resident dq dispatch round
+    GridOrder dq_order;   // grid order of the dq kernel (set by launch_attn_bwd)
 };
 
 // ev: optional events recorded on `stream` around each kernel launch
