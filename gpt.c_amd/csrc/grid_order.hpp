@@ -54,11 +54,23 @@ __device__ __forceinline__ void grid_position(const GridOrder &o, int nblk, int 
 // the co-resident rounds (ties: the largest smallest sum).  Cached per shape.
 template <typename Kernel>
 GridOrder choose_grid_order(int nblk, int bh_pad, Kernel kernel) {
-    GridOrder o{};
-    int dev = 0, cus_total = 0, per_cu = 0;
+    // Device properties and the kernel's occupancy, once per device (this
+    // runs on every launch, so no runtime queries after the first).
+    struct DeviceInfo {
+        int cus_total, per_cu;
+    };
+    static std::map<int, DeviceInfo> devices;
+    int dev = 0;
     hipCheck(hipGetDevice(&dev));
-    hipCheck(hipDeviceGetAttribute(&cus_total, hipDeviceAttributeMultiprocessorCount, dev));
-    hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0));
+    auto d = devices.find(dev);
+    if (d == devices.end()) {
+        DeviceInfo info{};
+        hipCheck(hipDeviceGetAttribute(&info.cus_total, hipDeviceAttributeMultiprocessorCount, dev));
+        hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&info.per_cu, kernel, 256, 0));
+        d = devices.emplace(dev, info).first;
+    }
+    GridOrder o{};
+    const int cus_total = d->second.cus_total, per_cu = d->second.per_cu;
     if (cus_total % kXcds != 0 || per_cu < 2) return o;
     const int cus = cus_total / kXcds, nbh_x = bh_pad / kXcds, M = nblk * nbh_x;
     const int rounds = std::min(per_cu, kOrderRounds);
