@@ -175,14 +175,77 @@ def copy_calibration(args):
     rt.sync()
 
 
+def decode_bench(args):
+    """C4: KV-cache decode at GPT-2 small's heads (B=1, C=768, H=12), one layer.
+
+    A 64-token prompt fills the caches, then 448 generated tokens (positions
+    64..511) are timed, one attention_decode_cuda_kernel call each, inputs
+    resident in HBM.  Beside it: the reference-literal step, gpt.c's
+    infer_gpt.c:339-351 recompute of the full 1024-token window through
+    attention_forward_cuda_kernel for every token.
+    """
+    B, C, H, L, prompt, last = 1, 768, 12, 1024, 64, 512
+    D = C // H
+    lib = gptc.load()
+    rt = gptc.Runtime(lib)
+    rt.init()
+    hip = Hip()
+    stream = rt.stream()
+    x = rt.normal((B, last, 3 * C), SEED_X)
+    rows = [rt.from_numpy(x[:, p:p + 1, :]) for p in range(last)]
+    kc, vc, out = rt.empty((B, H, L, D)), rt.empty((B, H, L, D)), rt.empty((B, 1, C))
+    for p in range(prompt):
+        lib.attention_decode_cuda_kernel(rows[p], kc, vc, p, H, out)
+    rt.sync()
+    hip.device_sync()
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for p in range(prompt, last):
+        lib.attention_decode_cuda_kernel(rows[p], kc, vc, p, H, out)
+    hip.record(b, stream)
+    steps = last - prompt
+    us = hip.elapsed_ms(a, b) * 1e3 / steps
+    # Compulsory bytes: every cached key and value row read once, the new row read, k, v and y written.
+    kv_bytes = sum(2 * (p + 1) * C * 4 for p in range(prompt, last))
+    io_bytes = steps * (3 * C + 2 * C + C) * 4
+    gbs = (kv_bytes + io_bytes) / (us * 1e-6 * steps) / 1e9
+
+    # Reference-literal: forward over the full window for every token.
+    xw = rt.from_numpy(rt.normal((B, L, 3 * C), SEED_X))
+    mask = rt.from_numpy(np.tril(np.ones((L, L), np.float32)))
+    caches = (gptc.TensorP * 4)(xw, rt.empty((B, L, C)), rt.empty((B, H, L)),
+                                rt.empty((lib.gptc_attention_state_floats(B, L, C, H),)))
+    yw = rt.empty((B, L, C))
+    for _ in range(args.warmup):
+        lib.attention_forward_cuda_kernel(xw, mask, H, caches, yw)
+    rt.sync()
+    hip.record(a, stream)
+    for _ in range(args.steps):
+        lib.attention_forward_cuda_kernel(xw, mask, H, caches, yw)
+    hip.record(b, stream)
+    win_us = hip.elapsed_ms(a, b) * 1e3 / args.steps
+    print(json.dumps({
+        "workload": "C4 KV-cache decode, B=1 C=768 H=12 (GPT-2 small heads), positions 64..511, one layer",
+        "us_per_step": round(us, 3), "GB_per_s": round(gbs, 1), "hbm_peak_GB_per_s": HBM_PEAK_GBS,
+        "bytes_per_step": round((kv_bytes + io_bytes) / steps),
+        "window_forward_us_per_step": round(win_us, 2),
+        "speedup_vs_window_recompute": round(win_us / us, 1),
+        "note": "latency bound at B=1: 4 L D flop and 8 L D bytes per head per step",
+    }), flush=True)
+    for t in rows + [kc, vc, out, xw, mask, yw, *caches[1:]]:
+        rt.free(t)
+    rt.sync()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
-    ap.add_argument("--workload", choices=["attention", "copy"], default="attention",
-                    help="copy: HBM copy of known size, to calibrate rocprof byte counters")
+    ap.add_argument("--workload", choices=["attention", "copy", "decode"], default="attention",
+                    help="copy: HBM copy of known size, to calibrate rocprof byte counters; "
+                         "decode: the C4 KV-cache decode step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
@@ -191,6 +254,9 @@ def main():
         print("bench.py: this build measures one GPU only (every (b, h) pair of causal attention is "
               "independent; see DESIGN.md for how the path shards). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "decode":
+        decode_bench(args)
+        return
     if args.workload == "copy":
         copy_calibration(args)
         return

@@ -289,3 +289,45 @@ extern "C" long long gptc_attention_state_floats(int B, int T, int C, int n_head
     const Dims d{B, T, C, n_heads, C / n_heads};
     return state_layout(d, false).total;
 }
+
+extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos,
+                                             const int n_heads, tensor_t *output) {
+    CHECK_ERROR(qkv == NULL || k_cache == NULL || v_cache == NULL || output == NULL,
+                "Expected qkv, k_cache, v_cache and output to be non-NULL.");
+    CHECK_ERROR(qkv->ndims != 3 || qkv->shape[1] != 1 || qkv->shape[2] % 3 != 0,
+                "Expected qkv of shape (B, 1, 3C) (the new token's row), but got %d dims.", qkv->ndims);
+    Dims d;
+    d.B = qkv->shape[0];
+    d.T = 1;
+    d.C = qkv->shape[2] / 3;
+    d.H = n_heads;
+    CHECK_ERROR(d.H <= 0, "Expected n_heads > 0, but got %d.", d.H);
+    d.D = d.C / d.H;
+    check_head_size(d);
+    for (const tensor_t *c : {static_cast<const tensor_t *>(k_cache), static_cast<const tensor_t *>(v_cache)})
+        CHECK_ERROR(c->ndims != 4 || c->shape[0] != d.B || c->shape[1] != d.H || c->shape[3] != d.D,
+                    "Expected k_cache and v_cache of shape (B, H, L, D) = (%d, %d, L, %d).", d.B, d.H, d.D);
+    const int L = k_cache->shape[2];
+    CHECK_ERROR(v_cache->shape[2] != L, "Expected k_cache and v_cache with the same length L, but got %d and %d.", L,
+                v_cache->shape[2]);
+    CHECK_ERROR(pos < 0 || pos >= L, "Expected 0 <= pos < L = %d, but got pos = %d.", L, pos);
+    CHECK_ERROR(pos + 1 > gptc::kDecMaxKeys, "Decode attends at most %d keys, but pos = %d.", gptc::kDecMaxKeys, pos);
+    CHECK_ERROR(output->length != d.B * d.C, "Expected output of B*C = %d elements, but got %d.", d.B * d.C,
+                output->length);
+    if (d.B == 0 || d.C == 0) return;
+
+    gptc::DecParams p{};
+    p.qkv = qkv->t;
+    p.k_cache = k_cache->t;
+    p.v_cache = v_cache->t;
+    p.out = output->t;
+    p.B = d.B;
+    p.H = d.H;
+    p.C = d.C;
+    p.D = d.D;
+    p.L = L;
+    p.pos = pos;
+    p.scale_log2 = gptc::kLog2e / std::sqrt(static_cast<float>(d.D));
+    p.full = d.D == gptc::kDPad && aligned16(k_cache->t) && aligned16(v_cache->t);
+    gptc::launch_attn_decode(p, gptc_stream_checked());
+}

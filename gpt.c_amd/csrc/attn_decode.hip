@@ -1,0 +1,154 @@
+// One decode step of causal self-attention with a KV cache: the new token's
+// q, k, v row (B, 1, 3C) is attended against keys 0..pos of (B, H, L, D)
+// K/V caches, after its own k, v are written at position pos.
+//
+// gpt.c has no KV cache: its inference loop (infer_gpt.c:339-351) runs the
+// whole block_size window through the model for every new token, and keeps
+// only row i-1 of the logits.  Under the causal rule that row of attention's
+// output depends on keys 0..i-1 only, so this kernel returns exactly the
+// row the window recompute produces (attention.c / Attention.c math:
+// softmax(q k^T / sqrt(D)) v), reading each cached key and value once.
+//
+// The work is HBM- and latency-bound (4 L D flop against 8 L D bytes per
+// (b, h)): one 1024-thread workgroup (16 waves) per (b, h), with as many row
+// loads in flight as the registers allow.
+//   phase 1  thread per key: t_j = (q . k_j) log2(e)/sqrt(D) into LDS;
+//   phase 2  workgroup max m and sum l of p_j = exp2(t_j - m);
+//   phase 3  wave per key row, lane per dim: o = sum_j p_j v_j (coalesced
+//            256-byte rows, 8 rows in flight per wave), then the 16 waves'
+//            partial sums are added.
+#include "attn_common.hpp"
+#include "attn_kernels.hpp"
+#include "hip_check.hpp"
+
+namespace gptc {
+
+namespace {
+
+constexpr int kDecThreads = 1024;
+constexpr int kDecWaves = kDecThreads / 64;
+
+__device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
+    // Wave reduction, then the wave results through LDS (a fixed order).
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(v, off, 64);
+        v = is_max ? fmaxf(v, o) : v + o;
+    }
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kDecWaves; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+    return r;
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParams a) {
+    extern __shared__ float dyn_lds[];  // scores: pos + 1 floats
+    __shared__ float q_s[kDPad], k_s[kDPad], v_s[kDPad];
+    __shared__ float o_s[kDecWaves][kDPad];
+    __shared__ float red[kDecWaves];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bh = blockIdx.x;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int D = a.D, n = a.pos + 1;
+
+    // The new row: q, k, v of head h; k and v also go into the caches at pos.
+    const float *row = a.qkv + static_cast<size_t>(b) * 3 * a.C + h * D;
+    float *kc = a.k_cache + static_cast<size_t>(bh) * a.L * D;
+    float *vc = a.v_cache + static_cast<size_t>(bh) * a.L * D;
+    if (tid < kDPad) {
+        const bool ok = tid < D;
+        q_s[tid] = ok ? row[tid] : 0.0f;
+        const float kn = ok ? row[a.C + tid] : 0.0f, vn = ok ? row[2 * a.C + tid] : 0.0f;
+        k_s[tid] = kn;
+        v_s[tid] = vn;
+        if (ok) {
+            kc[static_cast<size_t>(a.pos) * D + tid] = kn;
+            vc[static_cast<size_t>(a.pos) * D + tid] = vn;
+        }
+    }
+    __syncthreads();
+
+    // Phase 1: scores in log2 units.  Key pos (the last) comes from LDS, its
+    // cache row having just been written by this workgroup.  full: D == 64
+    // and 16-byte rows, so a key row is 16 float4 loads.
+    float q[kDPad];
+#pragma unroll
+    for (int d = 0; d < kDPad; ++d) q[d] = q_s[d];
+    float t_max = -INFINITY;
+    for (int j = tid; j < n; j += kDecThreads) {
+        float acc = 0.0f;
+        if (j == a.pos) {
+#pragma unroll
+            for (int d = 0; d < kDPad; ++d) acc = fmaf(q[d], k_s[d], acc);
+        } else if (a.full) {
+            const f32x4 *kr = reinterpret_cast<const f32x4 *>(kc + static_cast<size_t>(j) * D);
+#pragma unroll
+            for (int i = 0; i < kDPad / 4; ++i) {
+                const f32x4 k4 = kr[i];
+                acc = fmaf(q[4 * i], k4[0], acc);
+                acc = fmaf(q[4 * i + 1], k4[1], acc);
+                acc = fmaf(q[4 * i + 2], k4[2], acc);
+                acc = fmaf(q[4 * i + 3], k4[3], acc);
+            }
+        } else {
+            const float *kr = kc + static_cast<size_t>(j) * D;
+            for (int d = 0; d < D; ++d) acc = fmaf(q_s[d], kr[d], acc);
+        }
+        const float t = acc * a.scale_log2;
+        dyn_lds[j] = t;
+        t_max = fmaxf(t_max, t);
+    }
+    const float m = block_reduce(t_max, red, true);
+
+    // Phase 2: p_j = exp2(t_j - m) in place, and their sum.
+    float l_part = 0.0f;
+    for (int j = tid; j < n; j += kDecThreads) {
+        const float p = fast_exp2(dyn_lds[j] - m);
+        dyn_lds[j] = p;
+        l_part += p;
+    }
+    const float l = block_reduce(l_part, red, false);  // its barriers also publish the p_j
+
+    // Phase 3: wave w takes keys w, w + 16, ...; lane = dim.
+    constexpr int kUnroll = 8;
+    float o = 0.0f;
+    if (lane < D) {
+        int j = w;
+        // Keys below pos come from the cache, kUnroll rows in flight per lane.
+        for (; j + (kUnroll - 1) * kDecWaves < a.pos; j += kUnroll * kDecWaves) {
+            float v[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) v[u] = vc[static_cast<size_t>(j + u * kDecWaves) * D + lane];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) o = fmaf(dyn_lds[j + u * kDecWaves], v[u], o);
+        }
+        for (; j < n; j += kDecWaves) {
+            const float v = (j == a.pos) ? v_s[lane] : vc[static_cast<size_t>(j) * D + lane];
+            o = fmaf(dyn_lds[j], v, o);
+        }
+    }
+    o_s[w][lane] = o;
+    __syncthreads();
+    if (tid < D) {
+        float y = o_s[0][tid];
+#pragma unroll
+        for (int i = 1; i < kDecWaves; ++i) y += o_s[i][tid];
+        a.out[static_cast<size_t>(b) * a.C + h * D + tid] = y / l;
+    }
+}
+
+void launch_attn_decode(const DecParams &p, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(p.pos + 1) * sizeof(float);
+    attn_decode_kernel<<<dim3(p.B * p.H), dim3(kDecThreads), lds, stream>>>(p);
+    hipCheck(hipGetLastError());
+}
+
+}  // namespace gptc

@@ -65,6 +65,22 @@ struct BwdParams {
     GridOrder dq_order;   // grid order of the dq kernel (set by launch_attn_bwd)
 };
 
+// One KV-cache decode step (attn_decode.hip).
+struct DecParams {
+    const float *qkv;     // (B, 1, 3C): the new token's q | k | v
+    float *k_cache;       // (B, H, L, D); row pos is written
+    float *v_cache;       // (B, H, L, D); row pos is written
+    float *out;           // (B, 1, C)
+    int B, H, C, D, L;
+    int pos;              // position of the new token; keys 0 .. pos are attended
+    float scale_log2;     // log2(e) / sqrt(D)
+    bool full;            // D == kDPad and 16-byte aligned cache rows
+};
+
+constexpr int kDecMaxKeys = 8192;  // pos + 1 limit (the scores live in LDS)
+
+void launch_attn_decode(const DecParams &p, hipStream_t stream);
+
 // ev: optional events recorded on `stream` around each kernel launch
 // (forward: ev[0], ev[1]; backward: ev[0..1] around the delta kernel,
 // ev[2..3] around the dk/dv kernel, ev[4..5] around the dq kernel).

@@ -126,6 +126,7 @@ SIGNATURES = {
     "gptc_stream": (_vp, []),
     "gptc_set_kernel_events": (None, [ctypes.POINTER(_vp), _ci]),
     "gptc_attention_state_floats": (ctypes.c_longlong, [_ci, _ci, _ci, _ci]),
+    "attention_decode_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
     # rand.h
     "manual_seed": (None, [_vp, ctypes.c_uint]),
     "randint32": (ctypes.c_uint, [_vp]),

@@ -90,6 +90,31 @@ void attention_backward_cuda_kernel(
 );
 
 /*
+ * ---- KV-cache decode: no counterpart in the reference ----
+ *
+ * attention_decode_cuda_kernel(qkv, k_cache, v_cache, pos, n_heads, output)
+ *   One generation step of causal self-attention with a KV cache.  gpt.c's
+ *   inference loop (infer_gpt.c:339-351) has no cache: it runs the whole
+ *   window through attention_forward_cuda_kernel for every new token and
+ *   keeps one row.  This call returns that row directly.
+ *   qkv      (B, 1, 3C) device: the new token's q | k | v (the c_attn row).
+ *   k_cache, v_cache (B, H, L, D) device, the (B, H, T, D) layout of gpt.c's
+ *            attention caches (attention.c:105-120): rows 0 .. pos-1 hold the
+ *            earlier tokens' keys and values; this call writes the new
+ *            token's k and v into row pos.  0 <= pos < L, pos < 8192.
+ *   output   (B, 1, C) device: attention output of position pos, equal to row
+ *            pos of the forward over tokens 0 .. pos.
+ */
+void attention_decode_cuda_kernel(
+    const tensor_t *qkv,
+    tensor_t *k_cache,
+    tensor_t *v_cache,
+    const int pos,
+    const int n_heads,
+    tensor_t *output
+);
+
+/*
  * ---- extensions with no counterpart in the reference ----
  * gptc_stream(): the hipStream_t (as void*) every launch of this library is
  * ordered on; for callers that time or order their own work against it.

@@ -125,3 +125,17 @@ def test_fatal_error_gpu_call_before_runtime_init():
     r = run_c_snippet("lib.alloc_cuda(16)\nprint('survived')")
     assert r.returncode == 1 and "survived" not in r.stdout
     assert "runtime_init" in r.stderr
+
+
+def test_fatal_error_decode_position_past_cache():
+    r = run_c_snippet("""
+        import numpy as np
+        row = rt.from_numpy(np.zeros((1, 1, 24), np.float32), gptc.CPU)
+        kc = rt.from_numpy(np.zeros((1, 2, 4, 4), np.float32), gptc.CPU)
+        vc = rt.from_numpy(np.zeros((1, 2, 4, 4), np.float32), gptc.CPU)
+        out = rt.from_numpy(np.zeros((1, 1, 8), np.float32), gptc.CPU)
+        lib.attention_decode_cuda_kernel(row, kc, vc, 4, 2, out)
+        print('survived')
+    """)
+    assert r.returncode == 1 and "survived" not in r.stdout
+    assert "0 <= pos < L = 4" in r.stderr
