@@ -1,0 +1,178 @@
+// AdamW step and gradient zeroing over a list of tensors (replaces
+// kernels/src/cuda/AdamW.cu, semantics of kernels/src/cpu/AdamW.c:5-58):
+//   p -= lr wd p;  m = lerp(g, m, b1);  v = lerp(g^2, v, b2);
+//   p -= lr (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps)
+// with lerp(a, b, w) = fma(w, b, fma(-w, a, a)) and the bias corrections
+// computed on the host in float, as the reference does.
+// Multi-tensor launches: up to kListMax tensors per launch, their pointers
+// passed by value; each workgroup covers kBlockElems consecutive elements of
+// one tensor (a table of per-tensor first workgroups maps blockIdx to it).
+#include <cmath>
+#include "gpu_kernels.h"
+#include "ops_common.hpp"
+
+namespace gptc {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kListMax = 36;
+constexpr int kBlockElems = kThreads * 4 * 4;  // four 16-byte vectors per thread
+
+struct TensorList {
+    float *p[kListMax];
+    float *g[kListMax];
+    float *m[kListMax];
+    float *v[kListMax];
+    int len[kListMax];
+    int first_block[kListMax + 1];
+    unsigned vec_mask[(kListMax + 31) / 32];
+    int n;
+};
+
+struct AdamArgs {
+    float lr, beta1, beta2, wd, eps, bc1, bc2;
+};
+
+__device__ __forceinline__ float lerp_ref(float start, float end, float weight) {
+    return fmaf(weight, end, fmaf(-weight, start, start));
+}
+
+__device__ __forceinline__ void adam_one(float &p, float g, float &m, float &v, const AdamArgs &a) {
+    p -= a.lr * a.wd * p;
+    const float mn = lerp_ref(g, m, a.beta1);
+    const float vn = lerp_ref(g * g, v, a.beta2);
+    const float m_hat = mn / a.bc1;
+    const float v_hat = vn / a.bc2;
+    m = mn;
+    v = vn;
+    p -= a.lr * m_hat / (sqrtf(v_hat) + a.eps);
+}
+
+__device__ __forceinline__ int list_index(const TensorList &t) {
+    int i = 0;
+    while (i + 1 < t.n && static_cast<int>(blockIdx.x) >= t.first_block[i + 1]) ++i;
+    return i;
+}
+
+// kind 0: AdamW step; kind 1: zero the g tensors.
+template <int kKind>
+__global__ __launch_bounds__(kThreads) void multi_tensor_kernel(const TensorList t, const AdamArgs a) {
+    const int i = list_index(t);
+    const int64_t start = static_cast<int64_t>(blockIdx.x - t.first_block[i]) * kBlockElems;
+    const int64_t n = t.len[i];
+    const int64_t end = start + kBlockElems < n ? start + kBlockElems : n;
+    float *gp = t.g[i];
+    const bool vec = (t.vec_mask[i / 32] >> (i % 32)) & 1u;
+    if (vec) {
+        // Whole 16-byte vectors of [start, end); start is a multiple of 4.
+        const int64_t v_end = end / 4;
+        for (int64_t k = start / 4 + threadIdx.x; k < v_end; k += kThreads) {
+            if (kKind == 1) {
+                reinterpret_cast<f32x4_t *>(gp)[k] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            } else {
+                f32x4_t p4 = reinterpret_cast<f32x4_t *>(t.p[i])[k];
+                const f32x4_t g4 = reinterpret_cast<const f32x4_t *>(gp)[k];
+                f32x4_t m4 = reinterpret_cast<f32x4_t *>(t.m[i])[k];
+                f32x4_t v4 = reinterpret_cast<f32x4_t *>(t.v[i])[k];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float pe = p4[e], me = m4[e], ve = v4[e];
+                    adam_one(pe, g4[e], me, ve, a);
+                    p4[e] = pe;
+                    m4[e] = me;
+                    v4[e] = ve;
+                }
+                reinterpret_cast<f32x4_t *>(t.p[i])[k] = p4;
+                reinterpret_cast<f32x4_t *>(t.m[i])[k] = m4;
+                reinterpret_cast<f32x4_t *>(t.v[i])[k] = v4;
+            }
+        }
+        for (int64_t j = 4 * v_end + threadIdx.x; j < end; j += kThreads) {
+            if (kKind == 1) gp[j] = 0.0f;
+            else adam_one(t.p[i][j], gp[j], t.m[i][j], t.v[i][j], a);
+        }
+    } else {
+        for (int64_t j = start + threadIdx.x; j < end; j += kThreads) {
+            if (kKind == 1) gp[j] = 0.0f;
+            else adam_one(t.p[i][j], gp[j], t.m[i][j], t.v[i][j], a);
+        }
+    }
+}
+
+void check_pair(const tensor_t *a, const tensor_t *b, const char *an, const char *bn, int i) {
+    CHECK_ERROR(a == NULL || b == NULL, "Expected %s[%d] and %s[%d] to be tensors, but got NULL.", an, i, bn, i);
+    CHECK_ERROR(a->device != CUDA || b->device != CUDA, "Expected %s[%d] and %s[%d] on the GPU.", an, i, bn, i);
+    CHECK_ERROR(a->length != b->length, "Expected %s[%d] and %s[%d] to be of same length, but got %d != %d.", an, i,
+                bn, i, a->length, b->length);
+}
+
+template <int kKind>
+void run_lists(tensor_t **params, tensor_t **grads, tensor_t **m, tensor_t **v, int n, const AdamArgs &a) {
+    hipStream_t s = gptc_stream_checked();
+    int i = 0;
+    while (i < n) {
+        TensorList t{};
+        int blocks = 0;
+        while (i < n && t.n < kListMax) {
+            const tensor_t *g = grads[i];
+            const int len = g->length;
+            if (len > 0) {
+                const int k = t.n++;
+                t.g[k] = grads[i]->t;
+                bool vec = aligned16(t.g[k]);
+                if (kKind == 0) {
+                    t.p[k] = params[i]->t;
+                    t.m[k] = m[i]->t;
+                    t.v[k] = v[i]->t;
+                    vec = vec && aligned16(t.p[k]) && aligned16(t.m[k]) && aligned16(t.v[k]);
+                }
+                t.len[k] = len;
+                t.first_block[k] = blocks;
+                if (vec) t.vec_mask[k / 32] |= 1u << (k % 32);
+                blocks += (len + kBlockElems - 1) / kBlockElems;
+            }
+            ++i;
+        }
+        if (t.n == 0) continue;
+        t.first_block[t.n] = blocks;
+        multi_tensor_kernel<kKind><<<dim3(blocks), dim3(kThreads), 0, s>>>(t, a);
+        hipCheck(hipGetLastError());
+    }
+}
+
+}  // namespace
+
+}  // namespace gptc
+
+using namespace gptc;
+
+extern "C" void step_adamW_cuda_kernel(tensor_t **parameters, tensor_t **gradients, tensor_t **m, tensor_t **v,
+                                       const int n, const float lr, const float beta1, const float beta2,
+                                       const float weight_decay, const float eps, const int step) {
+    CHECK_ERROR(parameters == NULL || gradients == NULL || m == NULL || v == NULL,
+                "Expected parameters, gradients, m and v to be tensor lists, but got NULL.");
+    for (int i = 0; i < n; i++) {
+        check_pair(parameters[i], gradients[i], "parameters", "gradients", i);
+        check_pair(m[i], v[i], "m", "v", i);
+        check_pair(parameters[i], m[i], "parameters", "m", i);
+    }
+    AdamArgs a;
+    a.lr = lr;
+    a.beta1 = beta1;
+    a.beta2 = beta2;
+    a.wd = weight_decay;
+    a.eps = eps;
+    a.bc1 = 1.0f - powf(beta1, static_cast<float>(step));
+    a.bc2 = 1.0f - powf(beta2, static_cast<float>(step));
+    run_lists<0>(parameters, gradients, m, v, n, a);
+}
+
+extern "C" void zero_grad_adamW_cuda_kernel(tensor_t **gradients, const int n) {
+    CHECK_ERROR(gradients == NULL, "Expected gradients to be a tensor list, but got NULL.");
+    for (int i = 0; i < n; i++) {
+        CHECK_ERROR(gradients[i] == NULL, "Expected gradients[%d] to be a tensor, but got NULL.", i);
+        CHECK_ERROR(gradients[i]->device != CUDA, "Expected gradients[%d] on the GPU.", i);
+    }
+    run_lists<1>(nullptr, gradients, nullptr, nullptr, n, AdamArgs{});
+}

@@ -1,0 +1,14 @@
+// The library's rocBLAS handle, bound to its stream, and a row-major fp32
+// GEMM over raw device pointers (used by the Linear kernels and sgemm_cuda).
+#pragma once
+
+#include <rocblas/rocblas.h>
+
+// Created on first use; fatal if the runtime has not been initialised.
+rocblas_handle gptc_blas_handle();
+void gptc_blas_destroy();
+
+// Row-major C (M x N) = alpha * op(A) op(B) + beta * C, op = transpose when
+// trans_* == 1 (gpt.c's sgemm convention, kernels/src/cpu/Tensor.c:81-104).
+void gptc_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float *A, int lda, const float *B,
+                int ldb, float beta, float *C, int ldc);

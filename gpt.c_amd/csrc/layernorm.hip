@@ -1,0 +1,261 @@
+// LayerNorm over the last dimension (replaces kernels/src/cuda/LayerNorm.cu,
+// semantics of kernels/src/cpu/LayerNorm.c:5-124):
+//   forward   mean, var = E[x^2] - mean^2, rstd = 1/sqrt(var + eps),
+//             y = (x - mean) * rstd * W + b; mean and rstd go to cache[0..1];
+//   backward  dout += a g W + b' x + c' (per-row a = rstd and the two row sums
+//             of g x W and g W), dW += sum_rows g (a x - a mean), db += sum_rows g.
+// One wave per row, the row held in registers (lane j holds columns
+// j, j + 64, ...).  The backward's dW / db row sums go through a partial
+// buffer (one row per workgroup, its 4 waves combined in LDS) and a fixed-
+// order final pass, so results do not depend on scheduling.
+#include "gpu_kernels.h"
+#include "ops_common.hpp"
+
+namespace gptc {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxCols = 2048;  // 32 columns per lane
+
+template <int K>
+__global__ __launch_bounds__(kThreads) void layernorm_fwd_kernel(const float *__restrict__ x,
+                                                                const float *__restrict__ W,
+                                                                const float *__restrict__ b, float *__restrict__ y,
+                                                                float *__restrict__ mean_out,
+                                                                float *__restrict__ rstd_out, int rows, int C,
+                                                                float eps) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * kWaves + static_cast<int>(threadIdx.x / kWave);
+    if (row >= rows) return;
+    const float *xr = x + static_cast<int64_t>(row) * C;
+    float v[K];
+    float s = 0.0f, ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int j = lane + k * kWave;
+        v[k] = j < C ? xr[j] : 0.0f;
+        s += v[k];
+        ss += v[k] * v[k];
+    }
+    s = wave_sum(s);
+    ss = wave_sum(ss);
+    const float scale = 1.0f / C;
+    const float mean = s * scale;
+    const float var = ss * scale - mean * mean;
+    const float rstd = 1.0f / sqrtf(var + eps);
+    float *yr = y + static_cast<int64_t>(row) * C;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int j = lane + k * kWave;
+        if (j < C) {
+            const float n = (v[k] - mean) * rstd * W[j];
+            yr[j] = b != nullptr ? n + b[j] : n;
+        }
+    }
+    if (lane == 0) {
+        mean_out[row] = mean;
+        rstd_out[row] = rstd;
+    }
+}
+
+// Workgroup blockIdx.x owns rows [r0, r1); its waves take every 4th row.
+// partial: (2, gridDim.x, C) = dW then db sums of this workgroup.
+template <int K>
+__global__ __launch_bounds__(kThreads) void layernorm_bwd_kernel(
+    const float *__restrict__ g, const float *__restrict__ x, const float *__restrict__ mean_in,
+    const float *__restrict__ rstd_in, const float *__restrict__ W, float *__restrict__ dout,
+    float *__restrict__ partial, int rows, int C, int rows_per_block) {
+    extern __shared__ float red[];  // (kWaves, 2, C)
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int r0 = blockIdx.x * rows_per_block;
+    const int r1 = min(rows, r0 + rows_per_block);
+    const float scale = 1.0f / C;
+    float wv[K], dw[K], dbs[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int j = lane + k * kWave;
+        wv[k] = j < C ? W[j] : 0.0f;
+        dw[k] = 0.0f;
+        dbs[k] = 0.0f;
+    }
+    for (int row = r0 + w; row < r1; row += kWaves) {
+        const float *xr = x + static_cast<int64_t>(row) * C;
+        const float *gr = g + static_cast<int64_t>(row) * C;
+        float xv[K], gv[K];
+        float ds = 0.0f, dbacc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int j = lane + k * kWave;
+            xv[k] = j < C ? xr[j] : 0.0f;
+            gv[k] = j < C ? gr[j] : 0.0f;
+            ds += gv[k] * xv[k] * wv[k];
+            dbacc += gv[k] * wv[k];
+        }
+        ds = wave_sum(ds);
+        dbacc = wave_sum(dbacc);
+        const float mean = mean_in[row], a = rstd_in[row];
+        const float bn = -a * mean;
+        const float bb = (dbacc * mean - ds) * a * a * a * scale;
+        const float cc = -bb * mean - dbacc * a * scale;
+        float *dr = dout + static_cast<int64_t>(row) * C;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int j = lane + k * kWave;
+            if (j < C) {
+                dw[k] += gv[k] * (a * xv[k] + bn);
+                dbs[k] += gv[k];
+                dr[j] += a * gv[k] * wv[k] + bb * xv[k] + cc;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int j = lane + k * kWave;
+        if (j < C) {
+            red[(w * 2 + 0) * C + j] = dw[k];
+            red[(w * 2 + 1) * C + j] = dbs[k];
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < C; j += kThreads) {
+        float sw = red[j], sb = red[C + j];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) {
+            sw += red[(i * 2 + 0) * C + j];
+            sb += red[(i * 2 + 1) * C + j];
+        }
+        partial[static_cast<int64_t>(blockIdx.x) * C + j] = sw;
+        partial[(static_cast<int64_t>(gridDim.x) + blockIdx.x) * C + j] = sb;
+    }
+}
+
+// dW[j] += sum_p partial[0, p, j]; db[j] += sum_p partial[1, p, j] (db may be null).
+__global__ __launch_bounds__(kThreads) void layernorm_param_grad_kernel(const float *__restrict__ partial,
+                                                                       float *__restrict__ dW, float *__restrict__ db,
+                                                                       int parts, int C) {
+    const int j = blockIdx.x * kThreads + threadIdx.x;
+    if (j >= C) return;
+    float sw = 0.0f, sb = 0.0f;
+    for (int p = 0; p < parts; ++p) {
+        sw += partial[static_cast<int64_t>(p) * C + j];
+        sb += partial[(static_cast<int64_t>(parts) + p) * C + j];
+    }
+    dW[j] += sw;
+    if (db != nullptr) db[j] += sb;
+}
+
+int cols_per_lane(int C) {
+    const int k = (C + kWave - 1) / kWave;
+    if (k <= 4) return 4;
+    if (k <= 8) return 8;
+    if (k <= 12) return 12;
+    if (k <= 16) return 16;
+    if (k <= 25) return 25;
+    return 32;
+}
+
+template <template <int> class F, typename... Args>
+void by_cols(int C, Args... args) {
+    switch (cols_per_lane(C)) {
+        case 4: F<4>::run(args...); break;
+        case 8: F<8>::run(args...); break;
+        case 12: F<12>::run(args...); break;
+        case 16: F<16>::run(args...); break;
+        case 25: F<25>::run(args...); break;
+        default: F<32>::run(args...); break;
+    }
+}
+
+template <int K>
+struct FwdLaunch {
+    static void run(const float *x, const float *W, const float *b, float *y, float *mean, float *rstd, int rows,
+                    int C, float eps, hipStream_t s) {
+        layernorm_fwd_kernel<K><<<dim3((rows + kWaves - 1) / kWaves), dim3(kThreads), 0, s>>>(x, W, b, y, mean, rstd,
+                                                                                            rows, C, eps);
+        hipCheck(hipGetLastError());
+    }
+};
+
+template <int K>
+struct BwdLaunch {
+    static void run(const float *g, const float *x, const float *mean, const float *rstd, const float *W, float *dout,
+                    float *partial, int rows, int C, int parts, int rows_per_block, hipStream_t s) {
+        const size_t lds = sizeof(float) * kWaves * 2 * C;
+        layernorm_bwd_kernel<K><<<dim3(parts), dim3(kThreads), lds, s>>>(g, x, mean, rstd, W, dout, partial, rows, C,
+                                                                        rows_per_block);
+        hipCheck(hipGetLastError());
+    }
+};
+
+void check_cols(int C) {
+    CHECK_ERROR(C < 1 || C > kMaxCols, "LayerNorm supports 1 .. %d features, but got %d.", kMaxCols, C);
+}
+
+}  // namespace
+
+}  // namespace gptc
+
+using namespace gptc;
+
+extern "C" void layer_norm_forward_cuda_kernel(const tensor_t *W, const tensor_t *b, const tensor_t *input,
+                                               const float eps, tensor_t **cache, tensor_t *output) {
+    check_gpu(W, "W");
+    check_gpu(input, "input");
+    check_gpu(output, "output");
+    CHECK_ERROR(cache == NULL, "Expected **cache to be a tensor_t pointer, but got NULL.");
+    check_gpu(cache[0], "cache[0] (mean)");
+    check_gpu(cache[1], "cache[1] (rstd)");
+    const int C = last_dim(input), rows = leading_rows(input);
+    check_cols(C);
+    CHECK_ERROR(W->length != C, "Expected W to hold %d elements, but got %d.", C, W->length);
+    if (b != NULL) {
+        check_gpu(b, "b");
+        CHECK_ERROR(b->length != C, "Expected b to hold %d elements, but got %d.", C, b->length);
+    }
+    CHECK_ERROR(output->length != input->length, "Expected output to match input's %d elements.", input->length);
+    CHECK_ERROR(cache[0]->length < rows || cache[1]->length < rows, "Expected cache[0..1] to hold %d rows.", rows);
+    if (rows == 0) return;
+    hipStream_t s = gptc_stream_checked();
+    by_cols<FwdLaunch>(C, static_cast<const float *>(input->t), static_cast<const float *>(W->t),
+                       static_cast<const float *>(b != NULL ? b->t : nullptr), output->t, cache[0]->t, cache[1]->t,
+                       rows, C, eps, s);
+}
+
+extern "C" void layer_norm_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t **cache,
+                                                const tensor_t *W, tensor_t *dW, tensor_t *db, tensor_t *dout) {
+    check_gpu(global_grad, "global_grad");
+    CHECK_ERROR(cache == NULL, "Expected **cache to be a tensor_t pointer, but got NULL.");
+    check_gpu(cache[0], "cache[0] (mean)");
+    check_gpu(cache[1], "cache[1] (rstd)");
+    check_gpu(cache[2], "cache[2] (input)");
+    check_gpu(W, "W");
+    check_gpu(dW, "dW");
+    check_gpu(dout, "dout");
+    const int C = last_dim(global_grad), rows = leading_rows(global_grad);
+    check_cols(C);
+    CHECK_ERROR(W->length != C || dW->length != C, "Expected W and dW to hold %d elements.", C);
+    CHECK_ERROR(cache[2]->length != global_grad->length || dout->length != global_grad->length,
+                "Expected the cached input and dout to match global_grad's %d elements.", global_grad->length);
+    CHECK_ERROR(cache[0]->length < rows || cache[1]->length < rows, "Expected cache[0..1] to hold %d rows.", rows);
+    if (db != NULL) {
+        check_gpu(db, "db");
+        CHECK_ERROR(db->length != C, "Expected db to hold %d elements, but got %d.", C, db->length);
+    }
+    if (rows == 0) return;
+    hipStream_t s = gptc_stream_checked();
+    // About 8 rows per wave: 256 workgroups at GPT-2's 8192 rows.
+    int parts = (rows + 31) / 32;
+    if (parts > 1024) parts = 1024;
+    const int rows_per_block = (rows + parts - 1) / parts;
+    parts = (rows + rows_per_block - 1) / rows_per_block;
+    float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * 2 * static_cast<size_t>(parts) * C));
+    by_cols<BwdLaunch>(C, static_cast<const float *>(global_grad->t), static_cast<const float *>(cache[2]->t),
+                       static_cast<const float *>(cache[0]->t), static_cast<const float *>(cache[1]->t),
+                       static_cast<const float *>(W->t), dout->t, partial, rows, C, parts, rows_per_block, s);
+    layernorm_param_grad_kernel<<<dim3((C + kThreads - 1) / kThreads), dim3(kThreads), 0, s>>>(
+        partial, dW->t, db != NULL ? db->t : nullptr, parts, C);
+    hipCheck(hipGetLastError());
+    free_cuda(partial);
+}

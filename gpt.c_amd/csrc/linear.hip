@@ -1,0 +1,147 @@
+// Linear layer kernels, y = x W^T + b (replaces kernels/src/cuda/Linear.cu:40-95,
+// semantics of kernels/src/cpu/Linear.c:4-80):
+//   forward   one fp32 GEMM (rocBLAS) then a bias pass over y;
+//   backward  dx = g W (overwrites dout), dW += g^T x (GEMM with beta = 1),
+//             db += column sums of g.
+// The column sums are deterministic: workgroups sum fixed row ranges into a
+// partial buffer, and a second kernel adds the partials in a fixed order
+// (the reference uses one atomicAdd per workgroup and column).
+#include "blas.hpp"
+#include "gpu_kernels.h"
+#include "ops_common.hpp"
+
+namespace gptc {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// y[r, c] += b[c] over rows x cols; vec: cols % 4 == 0 and 16-byte aligned rows.
+__global__ __launch_bounds__(kThreads) void bias_add_kernel(float *__restrict__ y, const float *__restrict__ b,
+                                                           int64_t rows, int cols, bool vec) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    if (vec) {
+        const int c4 = cols / 4;
+        const int64_t n4 = rows * c4;
+        for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
+            const int c = static_cast<int>(i % c4);
+            f32x4_t v = reinterpret_cast<f32x4_t *>(y)[i];
+            const f32x4_t bb = reinterpret_cast<const f32x4_t *>(b)[c];
+            v += bb;
+            reinterpret_cast<f32x4_t *>(y)[i] = v;
+        }
+    } else {
+        const int64_t n = rows * cols;
+        for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) y[i] += b[i % cols];
+    }
+}
+
+// partial[blockIdx.y, c] = sum of g[r, c] over the rows r this workgroup
+// owns (r = blockIdx.y * 4 + wave, stepping 4 * gridDim.y).  A wave reads 64
+// consecutive columns of one row per step.
+__global__ __launch_bounds__(kThreads) void colsum_partial_kernel(const float *__restrict__ g,
+                                                                 float *__restrict__ partial, int rows, int cols) {
+    __shared__ float red[kThreads / kWave][kWave];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int c = blockIdx.x * kWave + lane;
+    float s = 0.0f;
+    if (c < cols)
+        for (int r = blockIdx.y * (kThreads / kWave) + w; r < rows; r += gridDim.y * (kThreads / kWave))
+            s += g[static_cast<int64_t>(r) * cols + c];
+    red[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && c < cols) {
+        float t = red[0][lane];
+#pragma unroll
+        for (int i = 1; i < kThreads / kWave; ++i) t += red[i][lane];
+        partial[static_cast<int64_t>(blockIdx.y) * cols + c] = t;
+    }
+}
+
+// out[c] += sum over p < parts of partial[p, c], in order of p.
+__global__ __launch_bounds__(kThreads) void colsum_final_kernel(const float *__restrict__ partial,
+                                                               float *__restrict__ out, int parts, int cols) {
+    const int c = blockIdx.x * kThreads + threadIdx.x;
+    if (c >= cols) return;
+    float t = 0.0f;
+    for (int p = 0; p < parts; ++p) t += partial[static_cast<int64_t>(p) * cols + c];
+    out[c] += t;
+}
+
+}  // namespace
+
+void launch_bias_add(float *y, const float *b, int64_t rows, int cols, hipStream_t s) {
+    const bool vec = (cols % 4) == 0 && aligned16(y) && aligned16(b);
+    const int64_t items = vec ? rows * (cols / 4) : rows * cols;
+    bias_add_kernel<<<dim3(blocks_for(items, kThreads * 4)), dim3(kThreads), 0, s>>>(y, b, rows, cols, vec);
+    hipCheck(hipGetLastError());
+}
+
+// out[c] += sum_r g[r, c] for a row-major (rows x cols) g, deterministic.
+void launch_column_sum_add(const float *g, float *out, int rows, int cols, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return;
+    const int cblocks = (cols + kWave - 1) / kWave;
+    int parts = 1024 / cblocks;
+    const int max_parts = (rows + 3) / 4;
+    if (parts > max_parts) parts = max_parts;
+    if (parts > 256) parts = 256;
+    if (parts < 1) parts = 1;
+    float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * static_cast<size_t>(parts) * cols));
+    colsum_partial_kernel<<<dim3(cblocks, parts), dim3(kThreads), 0, s>>>(g, partial, rows, cols);
+    hipCheck(hipGetLastError());
+    colsum_final_kernel<<<dim3((cols + kThreads - 1) / kThreads), dim3(kThreads), 0, s>>>(partial, out, parts, cols);
+    hipCheck(hipGetLastError());
+    free_cuda(partial);
+}
+
+}  // namespace gptc
+
+using namespace gptc;
+
+extern "C" void linear_forward_cuda_kernel(const tensor_t *W, const tensor_t *b, const tensor_t *input,
+                                           tensor_t *output) {
+    check_gpu(W, "W");
+    check_gpu(input, "input");
+    check_gpu(output, "output");
+    CHECK_ERROR(W->ndims != 2, "Expected W to be (out_features, in_features), but got %d dims.", W->ndims);
+    const int out_f = W->shape[0], in_f = W->shape[1];
+    CHECK_ERROR(last_dim(input) != in_f, "Expected input's last dimension to be %d, but got %d.", in_f,
+                last_dim(input));
+    const int rows = leading_rows(input);
+    CHECK_ERROR(static_cast<int64_t>(rows) * out_f != output->length,
+                "Expected output to hold %d x %d elements, but it holds %d.", rows, out_f, output->length);
+    if (b != NULL) {
+        check_gpu(b, "b");
+        CHECK_ERROR(b->length != out_f, "Expected b to hold %d elements, but got %d.", out_f, b->length);
+    }
+    hipStream_t s = gptc_stream_checked();
+    gptc_sgemm(0, 1, rows, out_f, in_f, 1.0f, input->t, in_f, W->t, in_f, 0.0f, output->t, out_f);
+    if (b != NULL && rows > 0) launch_bias_add(output->t, b->t, rows, out_f, s);
+}
+
+extern "C" void linear_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t *cache, const tensor_t *W,
+                                            tensor_t *dW, tensor_t *db, tensor_t *dout) {
+    check_gpu(global_grad, "global_grad");
+    check_gpu(cache, "cache");
+    check_gpu(W, "W");
+    check_gpu(dW, "dW");
+    check_gpu(dout, "dout");
+    CHECK_ERROR(W->ndims != 2, "Expected W to be (out_features, in_features), but got %d dims.", W->ndims);
+    const int out_f = W->shape[0], in_f = W->shape[1];
+    const int rows = leading_rows(global_grad);
+    CHECK_ERROR(last_dim(global_grad) != out_f, "Expected global_grad's last dimension to be %d, but got %d.", out_f,
+                last_dim(global_grad));
+    CHECK_ERROR(static_cast<int64_t>(rows) * in_f != cache->length || cache->length != dout->length,
+                "Expected the cached input and dout to hold %d x %d elements.", rows, in_f);
+    CHECK_ERROR(dW->length != W->length, "Expected dW to match W's %d elements, but got %d.", W->length, dW->length);
+    if (db != NULL) {
+        check_gpu(db, "db");
+        CHECK_ERROR(db->length != out_f, "Expected db to hold %d elements, but got %d.", out_f, db->length);
+    }
+    hipStream_t s = gptc_stream_checked();
+    // dx = g W : (rows x out) (out x in)
+    gptc_sgemm(0, 0, rows, in_f, out_f, 1.0f, global_grad->t, out_f, W->t, in_f, 0.0f, dout->t, in_f);
+    // dW += g^T x : (out x rows) (rows x in)
+    gptc_sgemm(1, 0, out_f, in_f, rows, 1.0f, global_grad->t, out_f, cache->t, in_f, 1.0f, dW->t, in_f);
+    if (db != NULL) launch_column_sum_add(global_grad->t, db->t, rows, out_f, s);
+}

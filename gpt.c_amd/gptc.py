@@ -107,6 +107,23 @@ SIGNATURES = {
     "copy_tensor_data_dispatch": (None, [TensorP, TensorP]),
     "attention_forward_dispatch": (None, [TensorP, TensorP, _ci, ctypes.POINTER(TensorP), TensorP]),
     "attention_backward_dispatch": (None, [TensorP, ctypes.POINTER(TensorP), _ci, TensorP]),
+    "saxpy_dispatch": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),
+    "sgemm_dispatch": (None, [_ci, _ci, _ci, _ci, _ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci, _cf, TensorP, _ci,
+                              _ci]),
+    "linear_forward_dispatch": (None, [TensorP, TensorP, TensorP, TensorP]),
+    "linear_backward_dispatch": (None, [TensorP, TensorP, TensorP, TensorP, TensorP, TensorP]),
+    "layer_norm_forward_dispatch": (None, [TensorP, TensorP, TensorP, _cf, ctypes.POINTER(TensorP), TensorP]),
+    "layer_norm_backward_dispatch": (None, [TensorP, ctypes.POINTER(TensorP), TensorP, TensorP, TensorP, TensorP]),
+    "gelu_forward_dispatch": (None, [TensorP, TensorP]),
+    "gelu_backward_dispatch": (None, [TensorP, TensorP, TensorP]),
+    "softmax_forward_dispatch": (None, [TensorP, TensorP]),
+    "softmax_backward_dispatch": (None, [TensorP, TensorP, TensorP]),
+    "embedding_forward_dispatch": (None, [TensorP, TensorP, TensorP]),
+    "embedding_backward_dispatch": (None, [TensorP, TensorP, TensorP]),
+    "cross_entropy_forward_dispatch": (None, [TensorP, TensorP, ctypes.POINTER(TensorP), TensorP]),
+    "cross_entropy_backward_dispatch": (None, [TensorP, ctypes.POINTER(TensorP), TensorP]),
+    "step_adamW_dispatch": (None, [ctypes.POINTER(TensorP)] * 4 + [_ci, _cf, _cf, _cf, _cf, _cf, _ci]),
+    "zero_grad_adamW_dispatch": (None, [ctypes.POINTER(TensorP), _ci]),
     # gpu_kernels.h
     "runtime_init_cuda": (None, []),
     "runtime_destroy_cuda": (None, []),
@@ -127,6 +144,42 @@ SIGNATURES = {
     "gptc_set_kernel_events": (None, [ctypes.POINTER(_vp), _ci]),
     "gptc_attention_state_floats": (ctypes.c_longlong, [_ci, _ci, _ci, _ci]),
     "attention_decode_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
+    "saxpy_cuda": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),
+    "sgemm_cuda": (None, [_ci, _ci, _ci, _ci, _ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci, _cf, TensorP, _ci,
+                          _ci]),
+    "sgemm_strided_batched_cuda": (None, [_ci, _ci, _ci, _ci, _ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci, _cf,
+                                          TensorP, _ci, _ci, _ci]),
+    "linear_forward_cuda_kernel": (None, [TensorP, TensorP, TensorP, TensorP]),
+    "linear_backward_cuda_kernel": (None, [TensorP, TensorP, TensorP, TensorP, TensorP, TensorP]),
+    "layer_norm_forward_cuda_kernel": (None, [TensorP, TensorP, TensorP, _cf, ctypes.POINTER(TensorP), TensorP]),
+    "layer_norm_backward_cuda_kernel": (None, [TensorP, ctypes.POINTER(TensorP), TensorP, TensorP, TensorP,
+                                               TensorP]),
+    "gelu_forward_cuda_kernel": (None, [TensorP, TensorP]),
+    "gelu_backward_cuda_kernel": (None, [TensorP, TensorP, TensorP]),
+    "softmax_forward_cuda_kernel": (None, [TensorP, TensorP]),
+    "softmax_backward_cuda_kernel": (None, [TensorP, TensorP, TensorP]),
+    "embedding_forward_cuda_kernel": (None, [TensorP, TensorP, TensorP]),
+    "embedding_backward_cuda_kernel": (None, [TensorP, TensorP, TensorP]),
+    "cross_entropy_forward_cuda_kernel": (None, [TensorP, TensorP, ctypes.POINTER(TensorP), TensorP]),
+    "cross_entropy_backward_cuda_kernel": (None, [TensorP, ctypes.POINTER(TensorP), TensorP]),
+    "step_adamW_cuda_kernel": (None, [ctypes.POINTER(TensorP)] * 4 + [_ci, _cf, _cf, _cf, _cf, _cf, _ci]),
+    "zero_grad_adamW_cuda_kernel": (None, [ctypes.POINTER(TensorP), _ci]),
+    # tensor.h (BLAS front ends)
+    "saxpy": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),
+    "sgemm": (None, [_ci, _ci, _ci, _ci, _ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci, _cf, TensorP, _ci, _ci]),
+    "uniform": (None, [TensorP, _cf, _cf]),
+    # model layers (linear.h, layer_norm.h, embedding.h, activation.h, loss.h, optim.h, blocks.h, transformer.h)
+    "Linear": (_vp, [_ci, _ci, _ci]),
+    "LayerNorm": (_vp, [_ci, _cf, _ci]),
+    "Embedding": (_vp, [_ci, _ci]),
+    "GELU": (_vp, []),
+    "Softmax": (_vp, []),
+    "CrossEntropyLoss": (_vp, []),
+    "AdamW": (_vp, [ctypes.POINTER(TensorP), ctypes.POINTER(TensorP), _ci, _cf, _cf, _cf, _cf, _cf]),
+    "MLP": (_vp, [_ci, _ci, _ci]),
+    "SelfAttention": (_vp, [_ci, _ci, _ci, _ci]),
+    "Block": (_vp, [_ci, _ci, _ci, _ci]),
+    "GPT2": (_vp, [_vp]),
     # rand.h
     "manual_seed": (None, [_vp, ctypes.c_uint]),
     "randint32": (ctypes.c_uint, [_vp]),
@@ -263,3 +316,165 @@ class AttentionLayer:
         if self.ptr:
             self._free_layer(self.ptr)
             self.ptr = None
+
+
+# ---- model layers (include/blocks.h, transformer.h, loss.h, optim.h) ----
+TensorPP = ctypes.POINTER(TensorP)
+_MODEL_FNS = ["forward", "backward", "description", "num_parameters", "free_layer", "free_cache", "parameters",
+              "gradients", "load_state_dict", "to"]
+
+
+class SelfAttentionT(ctypes.Structure):
+    """self_attention_t (include/blocks.h)."""
+    _fields_ = ([("n_embd", _ci), ("n_heads", _ci), ("use_bias", _ci), ("block_size", _ci),
+                 ("_num_param_tensors", _ci), ("_pad", ctypes.c_byte * 4),
+                 ("qkv", _vp), ("attn", _vp), ("c_proj", _vp)] + [(n, _vp) for n in _MODEL_FNS])
+
+
+class GPT2T(ctypes.Structure):
+    """gpt2_t (include/transformer.h)."""
+    _fields_ = ([("n_embd", _ci), ("n_heads", _ci), ("n_layers", _ci), ("block_size", _ci), ("vocab_size", _ci),
+                 ("_num_param_tensors", _ci), ("layers", _vp), ("wpe", _vp), ("wte", _vp), ("lm_head", _vp),
+                 ("ln_f", _vp)] + [(n, _vp) for n in _MODEL_FNS[:9]] +
+                [("fast_load_state_dict", _vp), ("to", _vp)])
+
+
+class GPT2Config(ctypes.Structure):
+    _fields_ = [("block_size", _ci), ("vocab_size", _ci), ("n_layers", _ci), ("n_heads", _ci), ("n_embd", _ci)]
+
+
+class CrossEntropyLossT(ctypes.Structure):
+    """cross_entropy_loss_t (include/loss.h)."""
+    _fields_ = [("softmax", _vp), ("cache", TensorP * 2), ("forward", _vp), ("backward", _vp), ("description", _vp),
+                ("num_parameters", _vp), ("free_layer", _vp), ("free_cache", _vp), ("to", _vp)]
+
+
+class AdamWT(ctypes.Structure):
+    """adamW_t (include/optim.h)."""
+    _fields_ = [("parameters", TensorPP), ("gradients", TensorPP), ("m", TensorPP), ("v", TensorPP),
+                ("lr", _cf), ("beta1", _cf), ("beta2", _cf), ("eps", _cf), ("weight_decay", _cf),
+                ("n_parameters", _ci), ("step_t", _ci), ("_pad", ctypes.c_byte * 4),
+                ("step", _vp), ("zero_grad", _vp), ("free_layer", _vp)]
+
+
+def _fn(addr, res, *args):
+    return ctypes.CFUNCTYPE(res, *args)(addr)
+
+
+class _Layer:
+    """A gpt.c layer object (forward/backward/parameters/... function pointers)."""
+
+    def __init__(self, rt, ptr, struct):
+        self.rt, self.ptr = rt, ctypes.cast(ptr, ctypes.POINTER(struct))
+        self.s = self.ptr.contents
+        self.raw = ctypes.c_void_p(ptr)
+
+    def forward(self, x):
+        return _fn(self.s.forward, TensorP, _vp, TensorP)(self.raw, x)
+
+    def backward(self, g):
+        return _fn(self.s.backward, TensorP, _vp, TensorP)(self.raw, g)
+
+    def n_params(self):
+        return self.s._num_param_tensors
+
+    def _tensor_list(self, fn):
+        """Call a parameters()/gradients() function pointer; the malloc'd array is
+        read as plain addresses (indexing it would alias its memory) and freed."""
+        arr = _fn(fn, _vp, _vp)(self.raw)
+        addrs = ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p))
+        vals = [addrs[i] for i in range(self.n_params())]
+        _libc_free(arr)
+        return [ctypes.cast(v, TensorP) for v in vals]
+
+    def parameters(self):
+        return self._tensor_list(self.s.parameters)
+
+    def gradients(self):
+        return self._tensor_list(self.s.gradients)
+
+    def to(self, device):
+        _fn(self.s.to, None, _vp, _ci)(self.raw, device)
+
+    def num_parameters(self):
+        return _fn(self.s.num_parameters, _ci, _vp)(self.raw)
+
+    def free_cache(self):
+        _fn(self.s.free_cache, None, _vp)(self.raw)
+
+    def free(self):
+        if self.raw:
+            _fn(self.s.free_layer, None, _vp)(self.raw)
+            self.raw = None
+
+    def load_arrays(self, arrays):
+        """load_state_dict from numpy arrays (host tensors, freed afterwards)."""
+        ts = [self.rt.from_numpy(a, CPU) for a in arrays]
+        arr = (TensorP * len(ts))(*ts)
+        _fn(self.s.load_state_dict, None, _vp, TensorPP)(self.raw, arr)
+        for t in ts:
+            self.rt.free(t)
+
+
+def _libc_free(p):
+    ctypes.CDLL(None).free(ctypes.cast(p, _vp))
+
+
+class SelfAttentionBlock(_Layer):
+    """SelfAttention(n_embd, n_heads, block_size, use_bias): qkv -> attention -> c_proj."""
+
+    def __init__(self, rt, n_embd, n_heads, block_size, use_bias=1):
+        super().__init__(rt, rt.lib.SelfAttention(n_embd, n_heads, block_size, use_bias), SelfAttentionT)
+
+
+class GPT2Model(_Layer):
+    """GPT2(config) driven through its function pointers."""
+
+    def __init__(self, rt, block_size, vocab_size, n_layers, n_heads, n_embd):
+        self.cfg = GPT2Config(block_size, vocab_size, n_layers, n_heads, n_embd)
+        super().__init__(rt, rt.lib.GPT2(ctypes.byref(self.cfg)), GPT2T)
+
+    def fast_load(self, arrays):
+        """fast_load_state_dict from numpy arrays in parameters() order."""
+        ts = [self.rt.from_numpy(a, CPU) for a in arrays]
+        arr = (TensorP * len(ts))(*ts)
+        _fn(self.s.fast_load_state_dict, None, _vp, TensorPP)(self.raw, arr)
+        for t in ts:
+            self.rt.free(t)
+
+
+class CrossEntropy:
+    def __init__(self, rt):
+        self.rt = rt
+        self.raw = ctypes.c_void_p(rt.lib.CrossEntropyLoss())
+        self.s = ctypes.cast(self.raw, ctypes.POINTER(CrossEntropyLossT)).contents
+
+    def forward(self, logits, targets):
+        return _fn(self.s.forward, TensorP, _vp, TensorP, TensorP)(self.raw, logits, targets)
+
+    def backward(self, g):
+        return _fn(self.s.backward, TensorP, _vp, TensorP)(self.raw, g)
+
+    def free(self):
+        _fn(self.s.free_layer, None, _vp)(self.raw)
+
+
+class AdamWOptimizer:
+    """AdamW(model.parameters(), model.gradients(), n, ...); the lists are
+    handed to (and freed by) the optimizer, as gpt.c's train_gpt.c does."""
+
+    def __init__(self, rt, model, lr=3e-4, beta1=0.9, beta2=0.99, eps=1e-8, weight_decay=0.0):
+        self.rt = rt
+        p = _fn(model.s.parameters, TensorPP, _vp)(model.raw)
+        g = _fn(model.s.gradients, TensorPP, _vp)(model.raw)
+        self.raw = ctypes.c_void_p(rt.lib.AdamW(p, g, model.n_params(), lr, beta1, beta2, eps, weight_decay))
+        self.s = ctypes.cast(self.raw, ctypes.POINTER(AdamWT)).contents
+
+    def step(self):
+        _fn(self.s.step, None, _vp)(self.raw)
+
+    def zero_grad(self):
+        _fn(self.s.zero_grad, None, _vp)(self.raw)
+
+    def free(self):
+        _fn(self.s.free_layer, None, _vp)(self.raw)

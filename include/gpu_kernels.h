@@ -90,6 +90,96 @@ void attention_backward_cuda_kernel(
 );
 
 /*
+ * ---- the rest of gpt.c's GPU back end (the other layers of the model) ----
+ * Same names, arguments and meaning as the CUDA entry points they replace;
+ * the semantics are those of gpt.c's CPU kernels (kernels/src/cpu/), which
+ * the CUDA ones follow.  Rows are the product of all dimensions but the
+ * last (B*T for gpt.c's (B, T, C) tensors).  Every device buffer is checked
+ * against the shapes before a launch (fatal on mismatch).
+ */
+
+/* BLAS, replaces kernels/src/cuda/Tensor.h:18-36 (Tensor.cu:132-206).
+ * Row-major, op = transpose when Trans* == 1.  The GEMMs are rocBLAS fp32
+ * (the reference runs cuBLAS in TF32 on sm >= 80), without atomic split-K,
+ * so results are deterministic.  saxpy requires incx, incy >= 1. */
+void saxpy_cuda(
+    const int n, const float alpha,
+    const tensor_t *x, const int offsetx, const int incx,
+    tensor_t *y, const int offsety, const int incy
+);
+void sgemm_cuda(
+    const int TransA, const int TransB, const int M, const int N, const int K,
+    const float alpha, const tensor_t *A, const int offsetA, const int lda,
+    const tensor_t *B, const int offsetB, const int ldb,
+    const float beta, tensor_t *C, const int offsetC, const int ldc
+);
+void sgemm_strided_batched_cuda(
+    const int TransA, const int TransB, const int M, const int N, const int K,
+    const float alpha, const tensor_t *A, const int lda, const int strideA,
+    const tensor_t *B, const int ldb, const int strideB,
+    const float beta, tensor_t *C, const int ldc, const int strideC, const int batch_count
+);
+
+/* Linear, replaces kernels/src/cuda/Linear.h:9-17 (cpu/Linear.c:4-80).
+ * forward: output = input W^T (+ b).  backward: dout = global_grad W
+ * (overwritten), dW += global_grad^T cache, db += column sums of global_grad
+ * (deterministic two-pass sum). */
+void linear_forward_cuda_kernel(const tensor_t *W, const tensor_t *b, const tensor_t *input, tensor_t *output);
+void linear_backward_cuda_kernel(
+    const tensor_t *global_grad, const tensor_t *cache, const tensor_t *W,
+    tensor_t *dW, tensor_t *db, tensor_t *dout
+);
+
+/* LayerNorm, replaces kernels/src/cuda/LayerNorm.h:9-25 (cpu/LayerNorm.c:5-124).
+ * cache[0] mean and cache[1] rstd (one per row), cache[2] the input.
+ * backward: dout += dx, dW += ..., db += ... (accumulate, as the reference).
+ * Up to 2048 features (fatal beyond). */
+void layer_norm_forward_cuda_kernel(
+    const tensor_t *W, const tensor_t *b, const tensor_t *input, const float eps,
+    tensor_t **cache, tensor_t *output
+);
+void layer_norm_backward_cuda_kernel(
+    const tensor_t *global_grad, const tensor_t **cache, const tensor_t *W,
+    tensor_t *dW, tensor_t *db, tensor_t *dout
+);
+
+/* GELU (tanh form), replaces kernels/src/cuda/GeLU.h:9-15 (cpu/GeLU.c:7-42).
+ * backward writes dout = global_grad * gelu'(cache). */
+void gelu_forward_cuda_kernel(const tensor_t *input, tensor_t *output);
+void gelu_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t *cache, tensor_t *dout);
+
+/* Softmax over the last dimension, replaces kernels/src/cuda/Softmax.h:9-15
+ * (cpu/Softmax.c:7-63).  cache = the forward's output. */
+void softmax_forward_cuda_kernel(const tensor_t *input, tensor_t *output);
+void softmax_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t *cache, tensor_t *dout);
+
+/* Embedding, replaces kernels/src/cuda/Embedding.h:9-19 (cpu/Embedding.c:3-47).
+ * Ids are floats truncated to int.  backward: dW[ids[i % len(ids)]] += g[i],
+ * deterministic (rows of one id are added in row order by one wave).  Ids
+ * outside [0, V): the forward writes a NaN row, the backward skips them. */
+void embedding_forward_cuda_kernel(const tensor_t *W, const tensor_t *input, tensor_t *output);
+void embedding_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t *cache, tensor_t *dW);
+
+/* Cross-entropy, replaces kernels/src/cuda/CrossEntropyLoss.h:9-20
+ * (cpu/CrossEntropyLoss.c:7-97).  forward: cache[0] (B,T,V) receives the
+ * log-softmax, output[0] the mean loss (a target outside [0, V) gives NaN).
+ * backward: cache[1] = targets; dout (B,T,V) is overwritten with
+ * (softmax - onehot(target)) * global_grad / (B*T). */
+void cross_entropy_forward_cuda_kernel(
+    const tensor_t *logits, const tensor_t *targets, tensor_t **cache, tensor_t *output
+);
+void cross_entropy_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t **cache, tensor_t *dout);
+
+/* AdamW, replaces kernels/src/cuda/AdamW.h:9-24 (cpu/AdamW.c:5-58).
+ * One launch per 36 tensors of the list. */
+void step_adamW_cuda_kernel(
+    tensor_t **parameters, tensor_t **gradients, tensor_t **m, tensor_t **v,
+    const int n, const float lr, const float beta1, const float beta2,
+    const float weight_decay, const float eps, const int step
+);
+void zero_grad_adamW_cuda_kernel(tensor_t **gradients, const int n);
+
+/*
  * ---- KV-cache decode: no counterpart in the reference ----
  *
  * attention_decode_cuda_kernel(qkv, k_cache, v_cache, pos, n_heads, output)

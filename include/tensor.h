@@ -40,6 +40,21 @@ tensor_t *arange(const int start, const int end, const int steps, const device_t
 
 void tensor_copy(tensor_t *dest, const tensor_t *src);
 
+/* y[offsety + i*incy] += alpha * x[offsetx + i*incx] and row-major
+ * C = alpha op(A) op(B) + beta C (op = transpose when Trans* == 1); both
+ * run on the GPU (reference tensor.h:62-68). */
+void saxpy(const int n, const float alpha, const tensor_t *x, const int offsetx, const int incx, tensor_t *y,
+           const int offsety, const int incy);
+void sgemm(
+    const int TransA, const int TransB, const int M, const int N, const int K,
+    const float alpha, const tensor_t *A, const int offsetA, const int lda,
+    const tensor_t *B, const int offsetB, const int ldb,
+    const float beta, tensor_t *C, const int offsetC, const int ldc
+);
+/* Fill a host tensor from the C library rand(), as gpt.c's uniform()
+ * (src/tensor.c:36-42,164-170) does, including its (high - low + 1) range. */
+void uniform(tensor_t *tensor, const float low, const float high);
+
 void shape(const tensor_t *tensor, char *shape);
 void view(tensor_t *tensor, const int *shape, const int n);
 

@@ -101,7 +101,9 @@ void oracle_set_threads(int n) {
     else if (g_threads64) g_threads64(n);
 }
 
-static void sgemm(int ta, int tb, int M, int N, int K, float alpha, const float *A, int lda, const float *Bm, int ldb,
+/* Row-major cblas_sgemm through the loaded OpenBLAS (ta/tb: kNoTrans or
+ * kTrans); also used by ops_oracle.c. */
+void oracle_sgemm(int ta, int tb, int M, int N, int K, float alpha, const float *A, int lda, const float *Bm, int ldb,
                   float beta, float *Cm, int ldc) {
     if (!g_lib) {
         fprintf(stderr, "[oracle] oracle_init was not called\n");
@@ -163,7 +165,7 @@ void oracle_attention_forward(const float *x, int B, int T, int C, int H, const 
             }
 
     for (long i = 0; i < (long)B * H; i++)
-        sgemm(kNoTrans, kTrans, T, T, D, scale, q + i * TD, D, k + i * TD, D, 0.0f, att + i * TT, T);
+        oracle_sgemm(kNoTrans, kTrans, T, T, D, scale, q + i * TD, D, k + i * TD, D, 0.0f, att + i * TT, T);
 
     for (long i = 0; i < (long)B * H; i++)
         for (int r = 0; r < T; r++) {
@@ -177,7 +179,7 @@ void oracle_attention_forward(const float *x, int B, int T, int C, int H, const 
     float *o = (float *)malloc(sizeof(float) * (size_t)B * H * TD + 64);
     if (!o) abort();
     for (long i = 0; i < (long)B * H; i++)
-        sgemm(kNoTrans, kNoTrans, T, D, T, 1.0f, att + i * TT, T, v + i * TD, D, 0.0f, o + i * TD, D);
+        oracle_sgemm(kNoTrans, kNoTrans, T, D, T, 1.0f, att + i * TT, T, v + i * TD, D, 0.0f, o + i * TD, D);
 
     for (int b = 0; b < B; b++)
         for (int t = 0; t < T; t++)
@@ -211,15 +213,15 @@ void oracle_attention_backward(const float *dy, int B, int T, int C, int H, cons
                        sizeof(float) * D);
 
     for (long i = 0; i < (long)B * H; i++) {
-        sgemm(kNoTrans, kTrans, T, T, D, 1.0f, g + i * TD, D, v + i * TD, D, 0.0f, datt + i * TT, T);
-        sgemm(kTrans, kNoTrans, T, D, T, 1.0f, att + i * TT, T, g + i * TD, D, 0.0f, dv + i * TD, D);
+        oracle_sgemm(kNoTrans, kTrans, T, T, D, 1.0f, g + i * TD, D, v + i * TD, D, 0.0f, datt + i * TT, T);
+        oracle_sgemm(kTrans, kNoTrans, T, D, T, 1.0f, att + i * TT, T, g + i * TD, D, 0.0f, dv + i * TD, D);
     }
 
     softmax_rows_backward(datt, att, (long)B * H * T, T);
 
     for (long i = 0; i < (long)B * H; i++) {
-        sgemm(kNoTrans, kNoTrans, T, D, T, scale, datt + i * TT, T, k + i * TD, D, 0.0f, dq + i * TD, D);
-        sgemm(kTrans, kNoTrans, T, D, T, scale, datt + i * TT, T, q + i * TD, D, 0.0f, dk + i * TD, D);
+        oracle_sgemm(kNoTrans, kNoTrans, T, D, T, scale, datt + i * TT, T, k + i * TD, D, 0.0f, dq + i * TD, D);
+        oracle_sgemm(kTrans, kNoTrans, T, D, T, scale, datt + i * TT, T, q + i * TD, D, 0.0f, dk + i * TD, D);
     }
 
     for (int b = 0; b < B; b++)
