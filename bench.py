@@ -237,15 +237,115 @@ def decode_bench(args):
     rt.sync()
 
 
+def gpt2_step_flops(B, T, L, C, V):
+    """Algorithmic flops of one GPT-2 training step: 2 per multiply-add of every
+    Linear (qkv 3C^2, c_proj C^2, c_fc 4C^2, mlp c_proj 4C^2 per layer, lm_head
+    C V), x3 for forward + the two backward products, plus the six causal
+    attention contractions per layer."""
+    linear = 2 * B * T * (L * 12 * C * C + C * V) * 3
+    attn = L * 6 * contraction_flops(B, T, 12, C // 12)
+    return linear + attn, attn
+
+
+def gpt2_bench(args):
+    """C3: one GPT-2 124M training step (train_gpt.c:481-521's loop body:
+    zero_grad, forward, CrossEntropyLoss forward and backward, model backward,
+    AdamW step) at B=8, T=1024, on the library's layer objects.  Weights are
+    C3's random init (N(0, 0.02) matrices and embeddings, zero biases,
+    LayerNorm weight 1); token ids and targets uniform in [0, 50257).  The
+    batch sits in HBM; each step copies it into the fresh id tensors that the
+    model and the loss take ownership of, as train_gpt.c's moves do."""
+    B, T, L, H, C, V, block = 8, 1024, 12, 12, 768, 50257, 1024
+    lib = gptc.load()
+    rt = gptc.Runtime(lib)
+    rt.init()
+    hip = Hip()
+    stream = rt.stream()
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from gpt2_oracle import param_shapes  # names and shapes only
+
+    params = []
+    for i, (name, shp) in enumerate(param_shapes(V, block, L, C)):
+        if name.endswith(("ln1.W", "ln2.W")) or name == "ln_f.W":
+            params.append(np.ones(shp, np.float32))
+        elif len(shp) == 1:
+            params.append(np.zeros(shp, np.float32))
+        else:
+            params.append(rt.normal(shp, 1000 + i, 0.0, 0.02))
+    rng = np.random.default_rng(SEED_X)
+    ids = rt.from_numpy(rng.integers(0, V, (B, T)).astype(np.float32))
+    tgs = rt.from_numpy(rng.integers(0, V, (B, T)).astype(np.float32))
+    ones = rt.from_numpy(np.ones((B, T), np.float32))
+    model = gptc.GPT2Model(rt, block, V, L, H, C)
+    model.fast_load(params)
+    del params
+    model.to(gptc.CUDA)
+    opt = gptc.AdamWOptimizer(rt, model, lr=3e-4, beta1=0.9, beta2=0.99, eps=1e-8, weight_decay=0.0)
+    loss_fn = gptc.CrossEntropy(rt)
+    losses_seen = []
+
+    def step(keep_loss=False):
+        x, t, g = rt.empty((B, T)), rt.empty((B, T)), rt.empty((B, T))
+        lib.tensor_copy(x, ids)
+        lib.tensor_copy(t, tgs)
+        lib.tensor_copy(g, ones)
+        opt.zero_grad()
+        logits = model.forward(x)
+        losses = loss_fn.forward(logits, t)
+        rt.free(logits)
+        g = loss_fn.backward(g)
+        g = model.backward(g)
+        if g:
+            rt.free(g)
+        opt.step()
+        if keep_loss:
+            losses_seen.append(float(rt.to_numpy(losses)[0]))
+        rt.free(losses)
+
+    log(f"[bench] C3 GPT-2 124M training step B={B} T={T}; warmup {args.warmup}, steps {args.steps}")
+    for i in range(args.warmup):
+        step(keep_loss=(i == 0))
+    rt.sync()
+    hip.device_sync()
+    a, b = hip.event(), hip.event()
+    t0 = time.perf_counter()
+    hip.record(a, stream)
+    for _ in range(args.steps):
+        step()
+    hip.record(b, stream)
+    ms = hip.elapsed_ms(a, b) / args.steps
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step(keep_loss=True)
+    rt.sync()
+    flops, attn_flops = gpt2_step_flops(B, T, L, C, V)
+    peak, cu, mhz, src = device_peak()
+    tflops = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "workload": "C3 GPT-2 124M training step (fwd + CrossEntropy + bwd + AdamW), B=8 T=1024, fp32",
+        "metric": "tokens/s", "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s",
+        "ms_per_step": round(ms, 3), "wall_ms_per_step": round(wall_ms, 3), "steps": args.steps,
+        "warmup": args.warmup, "tflops": round(tflops, 2), "pct_fp32_mfma_peak": round(100 * tflops / peak, 2),
+        "flops_per_step": flops, "attention_flops_per_step": attn_flops,
+        "loss_first_step": round(losses_seen[0], 6), "loss_after": round(losses_seen[-1], 6),
+        "dtype": "fp32", "data": "synthetic (uniform token ids, N(0,0.02) init)",
+    }), flush=True)
+    opt.free()
+    loss_fn.free()
+    model.free()
+    for t in (ids, tgs, ones):
+        rt.free(t)
+    rt.sync()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
-    ap.add_argument("--workload", choices=["attention", "copy", "decode"], default="attention",
+    ap.add_argument("--workload", choices=["attention", "copy", "decode", "gpt2"], default="attention",
                     help="copy: HBM copy of known size, to calibrate rocprof byte counters; "
-                         "decode: the C4 KV-cache decode step")
+                         "decode: the C4 KV-cache decode step; gpt2: the C3 GPT-2 124M training step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
@@ -256,6 +356,9 @@ def main():
         sys.exit(2)
     if args.workload == "decode":
         decode_bench(args)
+        return
+    if args.workload == "gpt2":
+        gpt2_bench(args)
         return
     if args.workload == "copy":
         copy_calibration(args)

@@ -1,8 +1,23 @@
-// HIP runtime of the library: device 0, one non-blocking stream, and
-// stream-ordered allocation from the device's default memory pool.
-// Replaces gpt.c's kernels/src/cuda/runtime.cu:16-52 and Alloc.cu:9-20
-// (no BLAS handle: the attention path uses no BLAS library).
+// HIP runtime of the library: device 0, one non-blocking stream, and a
+// stream-ordered caching allocator.  Replaces gpt.c's
+// kernels/src/cuda/runtime.cu:16-52 and Alloc.cu:9-20.
+//
+// Allocation.  gpt.c's layers allocate and free their activations and
+// gradients every step (hundreds of buffers per GPT-2 step).  hipFreeAsync
+// on this stack can block the host for milliseconds (tens of ms seen for
+// some frees in a GPT-2 step trace), which leaves the GPU idle.  So freed
+// blocks are kept in a cache keyed by size class and handed to the next
+// request of the same class.  Every launch, copy and fill of the library
+// runs on its one stream, so a block reused after free_cuda() is only
+// touched by work queued after everything that used it before: reuse needs
+// no event or synchronisation.  Size classes: multiples of 512 B up to
+// 1 MiB, multiples of 2 MiB above.  When the device runs out of memory the
+// cache is returned to the device and the request retried once.
 #include <cstdint>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include "blas.hpp"
 #include "gpu_kernels.h"
 #include "hip_check.hpp"
 #include "utils.h"
@@ -11,6 +26,35 @@ namespace {
 hipStream_t g_stream = nullptr;
 bool g_ready = false;
 bool g_pool_alloc = false;  // device supports stream-ordered allocation
+
+std::mutex g_alloc_mu;
+std::unordered_map<void *, size_t> g_live;  // block -> size class, in use
+std::multimap<size_t, void *> g_cached;     // size class -> free block
+size_t g_cached_bytes = 0;
+
+size_t size_class(size_t n) {
+    if (n == 0) n = 1;
+    constexpr size_t kSmall = 512, kLarge = 2u << 20, kSplit = 1u << 20;
+    return n <= kSplit ? (n + kSmall - 1) / kSmall * kSmall : (n + kLarge - 1) / kLarge * kLarge;
+}
+
+hipError_t device_alloc(void **p, size_t n) {
+    return g_pool_alloc ? hipMallocAsync(p, n, g_stream) : hipMalloc(p, n);
+}
+
+void device_free(void *p) {
+    if (g_pool_alloc)
+        hipCheck(hipFreeAsync(p, g_stream));
+    else
+        hipCheck(hipFree(p));
+}
+
+// Return every cached block to the device (caller holds g_alloc_mu).
+void release_cache() {
+    for (auto &kv : g_cached) device_free(kv.second);
+    g_cached.clear();
+    g_cached_bytes = 0;
+}
 }  // namespace
 
 hipStream_t gptc_stream_checked() {
@@ -29,9 +73,7 @@ extern "C" void runtime_init_cuda(void) {
     hipCheck(hipDeviceGetAttribute(&pools, hipDeviceAttributeMemoryPoolsSupported, 0));
     g_pool_alloc = pools != 0;
     if (g_pool_alloc) {
-        // Keep freed blocks in the pool: layers allocate and free their
-        // activations every step, and returning them to the driver at each
-        // synchronisation would turn every step into fresh mappings.
+        // Blocks that do leave the cache stay in the driver's pool.
         hipMemPool_t pool;
         hipCheck(hipDeviceGetDefaultMemPool(&pool, 0));
         uint64_t keep = UINT64_MAX;
@@ -42,6 +84,12 @@ extern "C" void runtime_init_cuda(void) {
 
 extern "C" void runtime_destroy_cuda(void) {
     if (!g_ready) return;
+    hipCheck(hipStreamSynchronize(g_stream));
+    gptc_blas_destroy();
+    {
+        std::lock_guard<std::mutex> lk(g_alloc_mu);
+        release_cache();
+    }
     hipCheck(hipStreamSynchronize(g_stream));
     hipCheck(hipStreamDestroy(g_stream));
     g_stream = nullptr;
@@ -57,21 +105,39 @@ extern "C" void *gptc_stream(void) {
 }
 
 extern "C" void *alloc_cuda(const size_t nbytes) {
-    hipStream_t s = gptc_stream_checked();
+    gptc_stream_checked();
+    const size_t cls = size_class(nbytes);
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    auto it = g_cached.find(cls);
     void *ptr = nullptr;
-    const size_t n = nbytes ? nbytes : 4;
-    if (g_pool_alloc)
-        hipCheck(hipMallocAsync(&ptr, n, s));
-    else
-        hipCheck(hipMalloc(&ptr, n));
+    if (it != g_cached.end()) {
+        ptr = it->second;
+        g_cached.erase(it);
+        g_cached_bytes -= cls;
+    } else {
+        hipError_t err = device_alloc(&ptr, cls);
+        if (err == hipErrorOutOfMemory && !g_cached.empty()) {
+            (void)hipGetLastError();  // clear the failed allocation's error
+            release_cache();
+            hipCheck(hipStreamSynchronize(g_stream));
+            err = device_alloc(&ptr, cls);
+        }
+        hipCheck(err);
+    }
+    g_live.emplace(ptr, cls);
     return ptr;
 }
 
 extern "C" void free_cuda(void *ptr) {
     if (ptr == nullptr) return;
-    hipStream_t s = gptc_stream_checked();
-    if (g_pool_alloc)
-        hipCheck(hipFreeAsync(ptr, s));
-    else
-        hipCheck(hipFree(ptr));
+    gptc_stream_checked();
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    auto it = g_live.find(ptr);
+    if (it == g_live.end()) {  // not from alloc_cuda: hand it back directly
+        device_free(ptr);
+        return;
+    }
+    g_cached.emplace(it->second, ptr);
+    g_cached_bytes += it->second;
+    g_live.erase(it);
 }
