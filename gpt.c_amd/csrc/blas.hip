@@ -106,6 +106,64 @@ void gptc_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, cons
                "sgemm");
 }
 
+namespace {
+
+// out[i] += p[0][i] + p[1][i] + ... + p[S-1][i], in that order.
+__global__ __launch_bounds__(kThreads) void add_partials_kernel(const float *__restrict__ p, float *__restrict__ out,
+                                                               int64_t n, int S, bool vec) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    if (vec) {
+        const int64_t n4 = n / 4;
+        for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
+            f32x4 acc = reinterpret_cast<const f32x4 *>(p)[i];
+            for (int s = 1; s < S; ++s) acc += reinterpret_cast<const f32x4 *>(p + s * n)[i];
+            f32x4 o = reinterpret_cast<f32x4 *>(out)[i];
+            o += acc;
+            reinterpret_cast<f32x4 *>(out)[i] = o;
+        }
+    } else {
+        for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+            float acc = p[i];
+            for (int s = 1; s < S; ++s) acc += p[s * n + i];
+            out[i] += acc;
+        }
+    }
+}
+
+}  // namespace
+
+void gptc_sgemm_wgrad(int out_f, int in_f, int rows, const float *g, const float *x, float *dW) {
+    if (out_f <= 0 || in_f <= 0) return;
+    // Output tiles of 128 x 128; below about two per CU the GEMM cannot fill
+    // 256 CUs, so the row (K) range is split into S slices computed as one
+    // strided-batched GEMM, and the slices are added in a fixed order.
+    const int64_t tiles = static_cast<int64_t>((out_f + 127) / 128) * ((in_f + 127) / 128);
+    int S = 1;
+    while (S < 8 && tiles * S < 512 && rows % (2 * S) == 0 && rows / (2 * S) >= 1024) S *= 2;
+    if (S == 1) {
+        gptc_sgemm(1, 0, out_f, in_f, rows, 1.0f, g, out_f, x, in_f, 1.0f, dW, in_f);
+        return;
+    }
+    hipStream_t s = gptc_stream_checked();
+    const int chunk = rows / S;
+    const int64_t n = static_cast<int64_t>(out_f) * in_f;
+    float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * static_cast<size_t>(n) * S));
+    const float one = 1.0f, zero = 0.0f;
+    // Column-major view: partial_b^T (in x out) = x_b^T (in x chunk) g_b (chunk x out).
+    blas_check(rocblas_sgemm_strided_batched(gptc_blas_handle(), rocblas_operation_none, rocblas_operation_transpose,
+                                             in_f, out_f, chunk, &one, x, in_f,
+                                             static_cast<rocblas_stride>(chunk) * in_f, g, out_f,
+                                             static_cast<rocblas_stride>(chunk) * out_f, &zero, partial, in_f, n, S),
+               "sgemm_strided_batched (weight gradient)");
+    int64_t blocks = (n / 4 + kThreads - 1) / kThreads;
+    if (blocks > 256 * 8) blocks = 256 * 8;
+    const bool vec = (n % 4) == 0 && (reinterpret_cast<uintptr_t>(dW) & 15) == 0;
+    add_partials_kernel<<<dim3(static_cast<int>(blocks < 1 ? 1 : blocks)), dim3(kThreads), 0, s>>>(partial, dW, n, S,
+                                                                                                   vec);
+    hipCheck(hipGetLastError());
+    free_cuda(partial);
+}
+
 extern "C" void sgemm_cuda(const int TransA, const int TransB, const int M, const int N, const int K,
                            const float alpha, const tensor_t *A, const int offsetA, const int lda, const tensor_t *B,
                            const int offsetB, const int ldb, const float beta, tensor_t *C, const int offsetC,

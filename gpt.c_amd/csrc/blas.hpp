@@ -12,3 +12,9 @@ void gptc_blas_destroy();
 // trans_* == 1 (gpt.c's sgemm convention, kernels/src/cpu/Tensor.c:81-104).
 void gptc_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float *A, int lda, const float *B,
                 int ldb, float beta, float *C, int ldc);
+
+// Weight gradient of a Linear layer: row-major dW (out_f x in_f) += g^T x,
+// g (rows x out_f), x (rows x in_f).  Deterministic: when the output has too
+// few tiles to fill the GPU, the rows are split into equal slices whose
+// products are added into dW in slice order.
+void gptc_sgemm_wgrad(int out_f, int in_f, int rows, const float *g, const float *x, float *dW);

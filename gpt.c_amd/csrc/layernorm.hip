@@ -131,21 +131,6 @@ __global__ __launch_bounds__(kThreads) void layernorm_bwd_kernel(
     }
 }
 
-// dW[j] += sum_p partial[0, p, j]; db[j] += sum_p partial[1, p, j] (db may be null).
-__global__ __launch_bounds__(kThreads) void layernorm_param_grad_kernel(const float *__restrict__ partial,
-                                                                       float *__restrict__ dW, float *__restrict__ db,
-                                                                       int parts, int C) {
-    const int j = blockIdx.x * kThreads + threadIdx.x;
-    if (j >= C) return;
-    float sw = 0.0f, sb = 0.0f;
-    for (int p = 0; p < parts; ++p) {
-        sw += partial[static_cast<int64_t>(p) * C + j];
-        sb += partial[(static_cast<int64_t>(parts) + p) * C + j];
-    }
-    dW[j] += sw;
-    if (db != nullptr) db[j] += sb;
-}
-
 int cols_per_lane(int C) {
     const int k = (C + kWave - 1) / kWave;
     if (k <= 4) return 4;
@@ -245,8 +230,8 @@ extern "C" void layer_norm_backward_cuda_kernel(const tensor_t *global_grad, con
     }
     if (rows == 0) return;
     hipStream_t s = gptc_stream_checked();
-    // About 8 rows per wave: 256 workgroups at GPT-2's 8192 rows.
-    int parts = (rows + 31) / 32;
+    // About 4 rows per wave: 512 workgroups (two per CU) at GPT-2's 8192 rows.
+    int parts = (rows + 15) / 16;
     if (parts > 1024) parts = 1024;
     const int rows_per_block = (rows + parts - 1) / parts;
     parts = (rows + rows_per_block - 1) / rows_per_block;
@@ -254,8 +239,7 @@ extern "C" void layer_norm_backward_cuda_kernel(const tensor_t *global_grad, con
     by_cols<BwdLaunch>(C, static_cast<const float *>(global_grad->t), static_cast<const float *>(cache[2]->t),
                        static_cast<const float *>(cache[0]->t), static_cast<const float *>(cache[1]->t),
                        static_cast<const float *>(W->t), dout->t, partial, rows, C, parts, rows_per_block, s);
-    layernorm_param_grad_kernel<<<dim3((C + kThreads - 1) / kThreads), dim3(kThreads), 0, s>>>(
-        partial, dW->t, db != NULL ? db->t : nullptr, parts, C);
-    hipCheck(hipGetLastError());
+    launch_add_column_partials(partial, dW->t, parts, C, s);
+    if (db != NULL) launch_add_column_partials(partial + static_cast<size_t>(parts) * C, db->t, parts, C, s);
     free_cuda(partial);
 }

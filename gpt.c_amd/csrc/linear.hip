@@ -1,8 +1,10 @@
 // Linear layer kernels, y = x W^T + b (replaces kernels/src/cuda/Linear.cu:40-95,
 // semantics of kernels/src/cpu/Linear.c:4-80):
 //   forward   one fp32 GEMM (rocBLAS) then a bias pass over y;
-//   backward  dx = g W (overwrites dout), dW += g^T x (GEMM with beta = 1),
-//             db += column sums of g.
+//   backward  dx = g W (overwrites dout), dW += g^T x, db += column sums of g.
+// dW's GEMM has a small output (out x in) and a long reduction (B*T rows):
+// it is split over row slices (one strided-batched GEMM) and the slices are
+// added into dW in a fixed order, so it fills the GPU and stays deterministic.
 // The column sums are deterministic: workgroups sum fixed row ranges into a
 // partial buffer, and a second kernel adds the partials in a fixed order
 // (the reference uses one atomicAdd per workgroup and column).
@@ -58,14 +60,28 @@ __global__ __launch_bounds__(kThreads) void colsum_partial_kernel(const float *_
     }
 }
 
-// out[c] += sum over p < parts of partial[p, c], in order of p.
-__global__ __launch_bounds__(kThreads) void colsum_final_kernel(const float *__restrict__ partial,
-                                                               float *__restrict__ out, int parts, int cols) {
-    const int c = blockIdx.x * kThreads + threadIdx.x;
-    if (c >= cols) return;
-    float t = 0.0f;
-    for (int p = 0; p < parts; ++p) t += partial[static_cast<int64_t>(p) * cols + c];
-    out[c] += t;
+constexpr int kPartialWaves = 8;
+
+// out[c] += sum over p < parts of partial[p, c].  A workgroup owns 64
+// columns; wave w adds rows p = w, w + 8, ... and the 8 wave sums are then
+// added in wave order, so the result does not depend on scheduling.
+__global__ __launch_bounds__(kPartialWaves * kWave) void add_column_partials_kernel(const float *__restrict__ partial,
+                                                                                  float *__restrict__ out, int parts,
+                                                                                  int cols) {
+    __shared__ float red[kPartialWaves][kWave];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int c = blockIdx.x * kWave + lane;
+    float s = 0.0f;
+    if (c < cols)
+        for (int p = w; p < parts; p += kPartialWaves) s += partial[static_cast<int64_t>(p) * cols + c];
+    red[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && c < cols) {
+        float t = red[0][lane];
+#pragma unroll
+        for (int i = 1; i < kPartialWaves; ++i) t += red[i][lane];
+        out[c] += t;
+    }
 }
 
 }  // namespace
@@ -89,9 +105,15 @@ void launch_column_sum_add(const float *g, float *out, int rows, int cols, hipSt
     float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * static_cast<size_t>(parts) * cols));
     colsum_partial_kernel<<<dim3(cblocks, parts), dim3(kThreads), 0, s>>>(g, partial, rows, cols);
     hipCheck(hipGetLastError());
-    colsum_final_kernel<<<dim3((cols + kThreads - 1) / kThreads), dim3(kThreads), 0, s>>>(partial, out, parts, cols);
-    hipCheck(hipGetLastError());
+    launch_add_column_partials(partial, out, parts, cols, s);
     free_cuda(partial);
+}
+
+void launch_add_column_partials(const float *partial, float *out, int parts, int cols, hipStream_t s) {
+    if (parts <= 0 || cols <= 0) return;
+    add_column_partials_kernel<<<dim3((cols + kWave - 1) / kWave), dim3(kPartialWaves * kWave), 0, s>>>(partial, out,
+                                                                                                     parts, cols);
+    hipCheck(hipGetLastError());
 }
 
 }  // namespace gptc
@@ -141,7 +163,7 @@ extern "C" void linear_backward_cuda_kernel(const tensor_t *global_grad, const t
     hipStream_t s = gptc_stream_checked();
     // dx = g W : (rows x out) (out x in)
     gptc_sgemm(0, 0, rows, in_f, out_f, 1.0f, global_grad->t, out_f, W->t, in_f, 0.0f, dout->t, in_f);
-    // dW += g^T x : (out x rows) (rows x in)
-    gptc_sgemm(1, 0, out_f, in_f, rows, 1.0f, global_grad->t, out_f, cache->t, in_f, 1.0f, dW->t, in_f);
+    // dW += g^T x : (out x rows) (rows x in), split over rows when the output is small
+    gptc_sgemm_wgrad(out_f, in_f, rows, global_grad->t, cache->t, dW->t);
     if (db != NULL) launch_column_sum_add(global_grad->t, db->t, rows, out_f, s);
 }
