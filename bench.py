@@ -247,6 +247,42 @@ def gpt2_step_flops(B, T, L, C, V):
     return linear + attn, attn
 
 
+def gpt2_cpu_baseline(rt, V, block, L, H, C):
+    """The oracle's GPT-2 step (C restatements of gpt.c's CPU kernels over
+    OpenBLAS) on a bounded sample of C3: one sequence (B=1, T=1024) through
+    the full 12-layer model, forward + loss + backward + AdamW, median of 2
+    after a warm-up."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as oracle_mod
+    from gpt2_oracle import GPT2Oracle, param_shapes
+    threads = min(16, os.cpu_count() or 1)
+    orc = oracle_mod.Oracle(threads=threads)
+    params = []
+    for i, (name, shp) in enumerate(param_shapes(V, block, L, C)):
+        if name.endswith(("ln1.W", "ln2.W")) or name == "ln_f.W":
+            params.append(np.ones(shp, np.float32))
+        elif len(shp) == 1:
+            params.append(np.zeros(shp, np.float32))
+        else:
+            params.append(rt.normal(shp, 1000 + i, 0.0, 0.02))
+    rng = np.random.default_rng(SEED_X)
+    ids, tg = rng.integers(0, V, (1, block)), rng.integers(0, V, (1, block))
+    g = GPT2Oracle(orc, params, L, H)
+    del params
+    times = []
+    for i in range(3):
+        t0 = time.perf_counter()
+        g.loss(g.forward(ids), tg)
+        g.backward()
+        g.step()
+        times.append(time.perf_counter() - t0)
+        log(f"[cpu] GPT-2 step {i}: {times[-1]:.2f} s")
+    sec = statistics.median(times[1:])
+    return {"value": round(block / sec, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"one GPT-2 124M training step at B=1 T={block} (1/8 of C3's batch), warm-up then median "
+                       f"of 2: {sec:.2f} s; OPENBLAS threads={threads}; {orc.blas_config}")}
+
+
 def gpt2_bench(args):
     """C3: one GPT-2 124M training step (train_gpt.c:481-521's loop body:
     zero_grad, forward, CrossEntropyLoss forward and backward, model backward,
@@ -320,6 +356,9 @@ def gpt2_bench(args):
     flops, attn_flops = gpt2_step_flops(B, T, L, C, V)
     peak, cu, mhz, src = device_peak()
     tflops = flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = gpt2_cpu_baseline(rt, V, block, L, H, C)
     print(json.dumps({
         "workload": "C3 GPT-2 124M training step (fwd + CrossEntropy + bwd + AdamW), B=8 T=1024, fp32",
         "metric": "tokens/s", "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s",
@@ -328,6 +367,7 @@ def gpt2_bench(args):
         "flops_per_step": flops, "attention_flops_per_step": attn_flops,
         "loss_first_step": round(losses_seen[0], 6), "loss_after": round(losses_seen[-1], 6),
         "dtype": "fp32", "data": "synthetic (uniform token ids, N(0,0.02) init)",
+        "cpu_baseline": cpu,
     }), flush=True)
     opt.free()
     loss_fn.free()
