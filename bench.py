@@ -247,6 +247,67 @@ def gpt2_step_flops(B, T, L, C, V):
     return linear + attn, attn
 
 
+def c4_bench(args):
+    """C4: greedy generation with GPT-2 124M (N(0, 0.02) init), B=1, a 64-token
+    uniform prompt, 448 new tokens to T=512.  Two loops on the same model:
+    the one-token KV-cache step (gptc_gpt2_decode) and infer_gpt.c's
+    reference context handling (the 1024-token window through GPT2.forward
+    for every token).  Both produce the same tokens (tests/test_generate_gpu.py);
+    here they are timed end to end, host loop included."""
+    from generation import kv_generate, window_generate
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from gpt2_oracle import param_shapes
+    V, block, L, H, C, prompt_len, total = 50257, 1024, 12, 12, 768, 64, 512
+    lib = gptc.load()
+    rt = gptc.Runtime(lib)
+    rt.init()
+    params = []
+    for i, (name, shp) in enumerate(param_shapes(V, block, L, C)):
+        if name.endswith(("ln1.W", "ln2.W")) or name == "ln_f.W":
+            params.append(np.ones(shp, np.float32))
+        elif len(shp) == 1:
+            params.append(np.zeros(shp, np.float32))
+        else:
+            params.append(rt.normal(shp, 1000 + i, 0.0, 0.02))
+    n_weights = sum(p.size for p in params)
+    model = gptc.GPT2Model(rt, block, V, L, H, C)
+    model.fast_load(params)
+    del params
+    model.to(gptc.CUDA)
+    prompt = np.random.default_rng(SEED_X).integers(0, V, prompt_len)
+    new = total - prompt_len
+    kv_generate(rt, model, prompt, prompt_len + 8, block)  # warm-up
+    rt.sync()
+    t0 = time.perf_counter()
+    toks, _ = kv_generate(rt, model, prompt, total, block)
+    rt.sync()
+    kv_s = time.perf_counter() - t0
+    window_generate(rt, model, prompt, prompt_len + 2, block)  # warm-up
+    rt.sync()
+    t0 = time.perf_counter()
+    wtoks, _ = window_generate(rt, model, prompt, total, block)
+    rt.sync()
+    win_s = time.perf_counter() - t0
+    model.free()
+    # Per generated token the decode path reads every weight once (the tied
+    # wte twice: embedding row and lm_head) and the cached keys and values.
+    kv_bytes = sum(2 * L * (p + 1) * C * 4 for p in range(prompt_len - 1, total - 1)) / new
+    step_bytes = n_weights * 4 + kv_bytes
+    # The prompt's 63 decode steps are part of the timed loop too.
+    per_tok = kv_s / (total - 1)
+    print(json.dumps({
+        "workload": "C4 greedy generation, GPT-2 124M (N(0,0.02) init), B=1, prompt 64, 448 new tokens to T=512",
+        "kv_cache": {"s_total": round(kv_s, 3), "ms_per_token": round(per_tok * 1e3, 3),
+                     "tokens_per_s": round(new / kv_s, 1), "bytes_per_step": round(step_bytes),
+                     "GB_per_s": round(step_bytes / per_tok / 1e9, 1), "hbm_peak_GB_per_s": HBM_PEAK_GBS},
+        "window_recompute": {"s_total": round(win_s, 3), "ms_per_token": round(win_s / new * 1e3, 3),
+                             "tokens_per_s": round(new / win_s, 1)},
+        "speedup": round(win_s / kv_s, 1), "same_tokens": bool(np.array_equal(toks, wtoks)),
+        "note": "host loop included (one token id read back per step, as infer_gpt.c does)",
+    }), flush=True)
+    rt.sync()
+
+
 def gpt2_cpu_baseline(rt, V, block, L, H, C):
     """The oracle's GPT-2 step (C restatements of gpt.c's CPU kernels over
     OpenBLAS) on a bounded sample of C3: one sequence (B=1, T=1024) through
@@ -383,9 +444,10 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c2")
-    ap.add_argument("--workload", choices=["attention", "copy", "decode", "gpt2"], default="attention",
+    ap.add_argument("--workload", choices=["attention", "copy", "decode", "gpt2", "c4"], default="attention",
                     help="copy: HBM copy of known size, to calibrate rocprof byte counters; "
-                         "decode: the C4 KV-cache decode step; gpt2: the C3 GPT-2 124M training step")
+                         "decode: the C4 KV-cache decode step; gpt2: the C3 GPT-2 124M training step; "
+                         "c4: C4 greedy generation with GPT-2 124M")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
@@ -399,6 +461,9 @@ def main():
         return
     if args.workload == "gpt2":
         gpt2_bench(args)
+        return
+    if args.workload == "c4":
+        c4_bench(args)
         return
     if args.workload == "copy":
         copy_calibration(args)

@@ -30,12 +30,22 @@ __global__ __launch_bounds__(kThreads) void layernorm_fwd_kernel(const float *__
     const int row = blockIdx.x * kWaves + static_cast<int>(threadIdx.x / kWave);
     if (row >= rows) return;
     const float *xr = x + static_cast<int64_t>(row) * C;
-    float v[K];
+    // Every load of the row and of W, b is issued before the first use (clamped
+    // indices, no branches around them), so a row costs one memory latency:
+    // at the decode step's single row that latency is the whole kernel.
+    float v[K], wv[K], bv[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int jc = min(lane + k * kWave, C - 1);
+        v[k] = xr[jc];
+        wv[k] = W[jc];
+        bv[k] = b != nullptr ? b[jc] : 0.0f;
+    }
     float s = 0.0f, ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int j = lane + k * kWave;
-        v[k] = j < C ? xr[j] : 0.0f;
+        const bool in = lane + k * kWave < C;
+        v[k] = in ? v[k] : 0.0f;
         s += v[k];
         ss += v[k] * v[k];
     }
@@ -50,8 +60,8 @@ __global__ __launch_bounds__(kThreads) void layernorm_fwd_kernel(const float *__
     for (int k = 0; k < K; ++k) {
         const int j = lane + k * kWave;
         if (j < C) {
-            const float n = (v[k] - mean) * rstd * W[j];
-            yr[j] = b != nullptr ? n + b[j] : n;
+            const float n = (v[k] - mean) * rstd * wv[k];
+            yr[j] = b != nullptr ? n + bv[k] : n;
         }
     }
     if (lane == 0) {

@@ -164,6 +164,13 @@ SIGNATURES = {
     "cross_entropy_backward_cuda_kernel": (None, [TensorP, ctypes.POINTER(TensorP), TensorP]),
     "step_adamW_cuda_kernel": (None, [ctypes.POINTER(TensorP)] * 4 + [_ci, _cf, _cf, _cf, _cf, _cf, _ci]),
     "zero_grad_adamW_cuda_kernel": (None, [ctypes.POINTER(TensorP), _ci]),
+    "gptc_linear_rows_cuda": (None, [TensorP, TensorP, TensorP, TensorP, _ci, TensorP]),
+    "gptc_embed_token_cuda": (None, [TensorP, TensorP, TensorP, _ci, TensorP]),
+    "gptc_argmax_cuda": (None, [TensorP, TensorP]),
+    # generate.h
+    "gptc_kv_cache_create": (_vp, [_vp, _ci, _ci]),
+    "gptc_kv_cache_free": (None, [_vp]),
+    "gptc_gpt2_decode": (TensorP, [_vp, _vp, TensorP, _ci]),
     # tensor.h (BLAS front ends)
     "saxpy": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),
     "sgemm": (None, [_ci, _ci, _ci, _ci, _ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci, _cf, TensorP, _ci, _ci]),
@@ -478,3 +485,21 @@ class AdamWOptimizer:
 
     def free(self):
         _fn(self.s.free_layer, None, _vp)(self.raw)
+
+
+class KVCache:
+    """gptc_kv_cache_create(model, B, L) and the one-token step gptc_gpt2_decode."""
+
+    def __init__(self, rt, model, B, L):
+        self.rt = rt
+        self.raw = ctypes.c_void_p(rt.lib.gptc_kv_cache_create(model.raw, B, L))
+        self.model = model
+
+    def decode(self, ids, pos):
+        """ids: device tensor (B, 1); returns the logits tensor (B, 1, V)."""
+        return self.rt.lib.gptc_gpt2_decode(self.model.raw, self.raw, ids, pos)
+
+    def free(self):
+        if self.raw:
+            self.rt.lib.gptc_kv_cache_free(self.raw)
+            self.raw = None

@@ -219,6 +219,23 @@ void attention_decode_cuda_kernel(
  * that the compact layout's forward expects (and otherwise re-points), so
  * that a layer can allocate it once at the right size.
  */
+/*
+ * ---- one-token model step (KV-cache generation): no counterpart in gpt.c ----
+ * gptc_linear_rows_cuda(W, b, x, residual, act, y)
+ *   y = act(x W^T + b) + residual for x with 1 .. 8 rows (the decode step's
+ *   activations); b and residual may be NULL; act 0 = none, 1 = GELU (the tanh
+ *   form of kernels/src/cpu/GeLU.c).  Each weight row is read once.
+ * gptc_embed_token_cuda(wte, wpe, ids, pos, out)
+ *   out (B, C) = wte[ids] + wpe[pos]; ids outside [0, V) give NaN rows.
+ * gptc_argmax_cuda(logits, ids)
+ *   ids[r] = first index of the maximum of logits row r (greedy decoding).
+ */
+void gptc_linear_rows_cuda(const tensor_t *W, const tensor_t *b, const tensor_t *x, const tensor_t *residual,
+                           const int act, tensor_t *y);
+void gptc_embed_token_cuda(const tensor_t *wte, const tensor_t *wpe, const tensor_t *ids, const int pos,
+                           tensor_t *out);
+void gptc_argmax_cuda(const tensor_t *logits, tensor_t *ids);
+
 void *gptc_stream(void);
 void gptc_set_kernel_events(void **events, int n);
 long long gptc_attention_state_floats(int B, int T, int C, int n_heads);

@@ -1,0 +1,160 @@
+"""GPU parity of KV-cache generation (C4) with the library's GPT-2.
+
+gpt.c generates by recomputing the whole block_size window for every token
+(infer_gpt.c:339-351).  The one-token step (gptc_gpt2_decode, include/
+generate.h) must give the same logits row.  Checked here:
+  * the small-row kernels (gptc_linear_rows_cuda with bias, GELU, residual;
+    gptc_embed_token_cuda; gptc_argmax_cuda) against the CPU oracle / numpy;
+  * decode logits of every position against the library's GPT2.forward over
+    the whole sequence and against the CPU oracle's forward (oracle/
+    gpt2_oracle.py), within 1e-4 x max(1, max|logits|), for B = 1 and B = 3;
+  * C4 itself: GPT-2 124M, N(0, 0.02) init, a 64-token uniform prompt, greedy
+    tokens up to T = 512: the KV-cache loop and infer_gpt.c's window loop
+    produce the same tokens, and the CPU oracle's forward over the generated
+    sequence picks every token whose top-2 logit margin exceeds 1e-3.
+"""
+import numpy as np
+import pytest
+
+import gptc
+import oracle as oracle_mod
+from generation import kv_generate, window_generate
+from gpt2_oracle import GPT2Oracle, param_shapes
+
+pytestmark = pytest.mark.gpu
+
+
+def check(name, got, ref, rel=1e-4, atol=0.0):
+    ref = np.asarray(ref, np.float64)
+    tol = atol + rel * max(1.0, float(np.abs(ref).max()))
+    err = float(np.abs(np.asarray(got, np.float64) - ref).max())
+    print(f"  {name}: max abs err {err:.3e} (tol {tol:.1e})")
+    assert np.isfinite(got).all(), name
+    assert err <= tol, f"{name}: {err:.3e} > {tol:.1e}"
+
+
+def c3_params(V, block, L, C, seed, std=0.02, jitter=0.0):
+    rng = np.random.default_rng(seed)
+    out = []
+    for name, shp in param_shapes(V, block, L, C):
+        if name.endswith(("ln1.W", "ln2.W")) or name == "ln_f.W":
+            p = np.ones(shp, np.float32)
+        elif len(shp) == 1:
+            p = np.zeros(shp, np.float32)
+        else:
+            p = (rng.standard_normal(shp) * std).astype(np.float32)
+        if jitter and len(shp) == 1:
+            p = (p + jitter * rng.standard_normal(shp)).astype(np.float32)
+        out.append(p)
+    return out
+
+
+def make_model(rt, params, V, block, L, H, C):
+    model = gptc.GPT2Model(rt, block, V, L, H, C)
+    model.fast_load(params)
+    model.to(gptc.CUDA)
+    return model
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(1, 768, 2304), (3, 768, 50257), (8, 3072, 768), (2, 5, 7)])
+def test_linear_rows(rt, oracle, rows, in_f, out_f):
+    ops = oracle_mod.Ops(oracle)
+    rng = np.random.default_rng(rows * 1000 + in_f)
+    W = (rng.standard_normal((out_f, in_f)) * 0.05).astype(np.float32)
+    b = rng.standard_normal(out_f).astype(np.float32)
+    x = rng.standard_normal((rows, 1, in_f)).astype(np.float32)
+    r = rng.standard_normal((rows, 1, out_f)).astype(np.float32)
+    ts = [rt.from_numpy(a) for a in (W, b, x, r)]
+    y = rt.empty((rows, 1, out_f))
+    lin = ops.linear_forward(W, b, x)
+    for act, res, ref in ((0, None, lin), (1, None, ops.gelu_forward(lin)), (0, ts[3], lin + r)):
+        rt.lib.gptc_linear_rows_cuda(ts[0], ts[1], ts[2], res, act, y)
+        check(f"rows={rows} act={act} residual={res is not None}", rt.to_numpy(y), ref, rel=2e-5, atol=1e-5)
+    rt.lib.gptc_linear_rows_cuda(ts[0], None, ts[2], None, 0, y)
+    check("no bias", rt.to_numpy(y), ops.linear_forward(W, None, x), rel=2e-5, atol=1e-5)
+    for t in ts + [y]:
+        rt.free(t)
+
+
+def test_embed_token_and_argmax(rt):
+    V, C, P = 50, 24, 10
+    rng = np.random.default_rng(3)
+    wte, wpe = rng.standard_normal((V, C)).astype(np.float32), rng.standard_normal((P, C)).astype(np.float32)
+    ids = np.array([[3], [49], [0]], np.float32)
+    tw, tp, ti = rt.from_numpy(wte), rt.from_numpy(wpe), rt.from_numpy(ids)
+    out = rt.empty((3, 1, C))
+    rt.lib.gptc_embed_token_cuda(tw, tp, ti, 7, out)
+    assert np.array_equal(rt.to_numpy(out)[:, 0], wte[[3, 49, 0]] + wpe[7])
+    logits = rng.standard_normal((4, 1, 50257)).astype(np.float32)
+    logits[1, 0, 17] = logits[1, 0, 40000] = 99.0  # tie: the first index wins
+    logits[2, 0, :] = -np.inf
+    logits[2, 0, 50256] = 0.0
+    tl, am = rt.from_numpy(logits), rt.empty((4,))
+    rt.lib.gptc_argmax_cuda(tl, am)
+    got = rt.to_numpy(am).astype(np.int64)
+    assert list(got) == [int(np.argmax(logits[0, 0])), 17, 50256, int(np.argmax(logits[3, 0]))]
+    for t in (tw, tp, ti, out, tl, am):
+        rt.free(t)
+
+
+@pytest.mark.parametrize("V,block,L,H,C,B,T", [
+    (97, 48, 2, 2, 64, 1, 40),
+    (97, 48, 2, 2, 64, 3, 33),       # three sequences in one step
+    (50257, 1024, 1, 12, 768, 1, 70),  # GPT-2 small's widths, one layer
+])
+def test_decode_logits_match_forward_and_oracle(rt, oracle, V, block, L, H, C, B, T):
+    print(f"case decode V={V} L={L} H={H} C={C} B={B} T={T}")
+    params = c3_params(V, block, L, C, seed=V + T, std=0.05, jitter=0.05)
+    model = make_model(rt, params, V, block, L, H, C)
+    rng = np.random.default_rng(T)
+    seq = rng.integers(0, V, (B, T))
+    # decode every position
+    cache = gptc.KVCache(rt, model, B, T)
+    dec = np.empty((B, T, V), np.float32)
+    for pos in range(T):
+        ids = rt.from_numpy(seq[:, pos:pos + 1].astype(np.float32))
+        lt = cache.decode(ids, pos)
+        dec[:, pos] = rt.to_numpy(lt)[:, 0]
+        rt.free(lt)
+        rt.free(ids)
+    cache.free()
+    # the library's full forward over the sequence
+    lt = model.forward(rt.from_numpy(seq.astype(np.float32)))
+    fwd = rt.to_numpy(lt)
+    rt.free(lt)
+    model.free_cache()
+    model.free()
+    check("decode vs forward", dec, fwd)
+    ref = GPT2Oracle(oracle, params, L, H).forward(seq)
+    check("decode vs oracle", dec, ref)
+
+
+def test_c4_greedy_generation(rt, oracle):
+    """C4: GPT-2 124M, N(0, 0.02) init, B = 1, 64-token prompt, greedy to T = 512."""
+    V, block, L, H, C = 50257, 1024, 12, 12, 768
+    params = c3_params(V, block, L, C, seed=1337)
+    model = make_model(rt, params, V, block, L, H, C)
+    prompt = np.random.default_rng(1338).integers(0, V, 64)
+    total = 512
+    kv_tokens, kv_rows = kv_generate(rt, model, prompt, total, block, keep_logits=True)
+    win_tokens, win_rows = window_generate(rt, model, prompt, total, block, keep_logits=True)
+    model.free()
+    kv_rows, win_rows = np.array(kv_rows), np.array(win_rows)
+    check("decode logits vs window logits (first 16 generated)", kv_rows[:16], win_rows[:16])
+    same = kv_tokens == win_tokens
+    if not same.all():
+        first = int(np.argmin(same))
+        top2 = np.sort(win_rows[first - 64])[-2:]
+        print(f"  first divergence at token {first}, window top-2 margin {top2[1] - top2[0]:.3e}")
+        assert top2[1] - top2[0] < 1e-4, "tokens differ where the choice was not a near-tie"
+    else:
+        print(f"  all {total - 64} generated tokens agree")
+    # The CPU oracle over the generated sequence: teacher-forced greedy picks.
+    logits = GPT2Oracle(oracle, params, L, H).forward(kv_tokens[None, :total - 1])[0]
+    srt = np.sort(logits[63:], axis=-1)
+    margin = srt[:, -1] - srt[:, -2]
+    picks = np.argmax(logits[63:], axis=-1)
+    firm = margin > 1e-3
+    print(f"  oracle: {int(firm.sum())} of {firm.size} picks with margin > 1e-3")
+    assert firm.mean() > 0.9
+    assert np.array_equal(picks[firm], kv_tokens[64:][firm])
