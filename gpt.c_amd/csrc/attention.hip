@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <initializer_list>
 #include "attn_kernels.hpp"
+#include "ops_common.hpp"
 #include "gpu_kernels.h"
 #include "hip_check.hpp"
 #include "utils.h"
@@ -290,8 +291,13 @@ extern "C" long long gptc_attention_state_floats(int B, int T, int C, int n_head
     return state_layout(d, false).total;
 }
 
-extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos,
-                                             const int n_heads, tensor_t *output) {
+namespace {
+
+// Shape checks and launch of the decode step; the position comes from the
+// host (pos, checked here) or from device memory (pos_dev, checked by the
+// kernel, for graph replays).
+void decode_step(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos, const int *pos_dev,
+                 const int n_heads, tensor_t *output) {
     CHECK_ERROR(qkv == NULL || k_cache == NULL || v_cache == NULL || output == NULL,
                 "Expected qkv, k_cache, v_cache and output to be non-NULL.");
     CHECK_ERROR(qkv->ndims != 3 || qkv->shape[1] != 1 || qkv->shape[2] % 3 != 0,
@@ -310,8 +316,14 @@ extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_ca
     const int L = k_cache->shape[2];
     CHECK_ERROR(v_cache->shape[2] != L, "Expected k_cache and v_cache with the same length L, but got %d and %d.", L,
                 v_cache->shape[2]);
-    CHECK_ERROR(pos < 0 || pos >= L, "Expected 0 <= pos < L = %d, but got pos = %d.", L, pos);
-    CHECK_ERROR(pos + 1 > gptc::kDecMaxKeys, "Decode attends at most %d keys, but pos = %d.", gptc::kDecMaxKeys, pos);
+    if (pos_dev == nullptr) {
+        CHECK_ERROR(pos < 0 || pos >= L, "Expected 0 <= pos < L = %d, but got pos = %d.", L, pos);
+        CHECK_ERROR(pos + 1 > gptc::kDecMaxKeys, "Decode attends at most %d keys, but pos = %d.", gptc::kDecMaxKeys,
+                    pos);
+    } else {
+        CHECK_ERROR(L > gptc::kDecMaxKeys, "Decode with a device-side position takes caches of at most %d rows.",
+                    gptc::kDecMaxKeys);
+    }
     CHECK_ERROR(output->length != d.B * d.C, "Expected output of B*C = %d elements, but got %d.", d.B * d.C,
                 output->length);
     if (d.B == 0 || d.C == 0) return;
@@ -327,7 +339,20 @@ extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_ca
     p.D = d.D;
     p.L = L;
     p.pos = pos;
+    p.pos_dev = pos_dev;
     p.scale_log2 = gptc::kLog2e / std::sqrt(static_cast<float>(d.D));
     p.full = d.D == gptc::kDPad && aligned16(k_cache->t) && aligned16(v_cache->t);
     gptc::launch_attn_decode(p, gptc_stream_checked());
+}
+
+}  // namespace
+
+extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos,
+                                             const int n_heads, tensor_t *output) {
+    decode_step(qkv, k_cache, v_cache, pos, nullptr, n_heads, output);
+}
+
+void gptc::attention_decode_devpos(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int *pos_dev,
+                                   const int n_heads, tensor_t *output) {
+    decode_step(qkv, k_cache, v_cache, 0, pos_dev, n_heads, output);
 }

@@ -48,16 +48,20 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 }  // namespace
 
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParams a) {
-    extern __shared__ float dyn_lds[];  // scores: pos + 1 floats
+    extern __shared__ float dyn_lds[];  // scores: pos + 1 floats (L with a device-side position)
     __shared__ float q_s[kDPad], k_s[kDPad], v_s[kDPad];
     __shared__ float o_s[kDecWaves][kDPad];
     __shared__ float red[kDecWaves];
 
+    // A device-side position (graph replays) is checked here, since the host
+    // could not: out of [0, L) the workgroup does nothing.
+    const int pos = a.pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*a.pos_dev) : a.pos;
+    if (pos < 0 || pos >= a.L) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H;
-    const int D = a.D, n = a.pos + 1;
+    const int D = a.D, n = pos + 1;
 
     // The new row: q, k, v of head h; k and v also go into the caches at pos.
     const float *row = a.qkv + static_cast<size_t>(b) * 3 * a.C + h * D;
@@ -70,8 +74,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
         k_s[tid] = kn;
         v_s[tid] = vn;
         if (ok) {
-            kc[static_cast<size_t>(a.pos) * D + tid] = kn;
-            vc[static_cast<size_t>(a.pos) * D + tid] = vn;
+            kc[static_cast<size_t>(pos) * D + tid] = kn;
+            vc[static_cast<size_t>(pos) * D + tid] = vn;
         }
     }
     __syncthreads();
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
     float t_max = -INFINITY;
     for (int j = tid; j < n; j += kDecThreads) {
         float acc = 0.0f;
-        if (j == a.pos) {
+        if (j == pos) {
 #pragma unroll
             for (int d = 0; d < kDPad; ++d) acc = fmaf(q[d], k_s[d], acc);
         } else if (a.full) {
@@ -123,7 +127,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
     if (lane < D) {
         int j = w;
         // Keys below pos come from the cache, kUnroll rows in flight per lane.
-        for (; j + (kUnroll - 1) * kDecWaves < a.pos; j += kUnroll * kDecWaves) {
+        for (; j + (kUnroll - 1) * kDecWaves < pos; j += kUnroll * kDecWaves) {
             float v[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) v[u] = vc[static_cast<size_t>(j + u * kDecWaves) * D + lane];
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
             for (int u = 0; u < kUnroll; ++u) o = fmaf(dyn_lds[j + u * kDecWaves], v[u], o);
         }
         for (; j < n; j += kDecWaves) {
-            const float v = (j == a.pos) ? v_s[lane] : vc[static_cast<size_t>(j) * D + lane];
+            const float v = (j == pos) ? v_s[lane] : vc[static_cast<size_t>(j) * D + lane];
             o = fmaf(dyn_lds[j], v, o);
         }
     }
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
 }
 
 void launch_attn_decode(const DecParams &p, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(p.pos + 1) * sizeof(float);
+    const size_t lds = static_cast<size_t>(p.pos_dev != nullptr ? p.L : p.pos + 1) * sizeof(float);
     attn_decode_kernel<<<dim3(p.B * p.H), dim3(kDecThreads), lds, stream>>>(p);
     hipCheck(hipGetLastError());
 }

@@ -73,6 +73,8 @@ struct DecParams {
     float *out;           // (B, 1, C)
     int B, H, C, D, L;
     int pos;              // position of the new token; keys 0 .. pos are attended
+    const int *pos_dev;   // if set, the position is read from device memory instead
+                          // (graph replays); the score buffer is then sized for L keys
     float scale_log2;     // log2(e) / sqrt(D)
     bool full;            // D == kDPad and 16-byte aligned cache rows
 };

@@ -27,64 +27,179 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(kGeluBeta * (x + cube)));
 }
 
-// One wave per output feature o: acc[r] = W[o, :] . x[r, :] for r < rows.
-template <bool kVec>
-__global__ __launch_bounds__(kThreads) void linear_rows_kernel(const float *__restrict__ W,
-                                                              const float *__restrict__ b,
-                                                              const float *__restrict__ x,
-                                                              const float *__restrict__ res, float *__restrict__ y,
-                                                              int rows, int in_f, int out_f, int act) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int o = blockIdx.x * kWaves + static_cast<int>(threadIdx.x / kWave);
-    if (o >= out_f) return;
-    const float *w = W + static_cast<int64_t>(o) * in_f;
+struct RowsArgs {
+    const float *W, *b, *x, *res;
+    float *y;
+    const float *ln_w, *ln_b;  // LayerNorm of x fused in front (ln_w set)
+    float eps;
+    int rows, in_f, out_f, act;
+};
+
+// The 4 waves of a workgroup own `kOuts` output features; for each, the
+// kSplit = 4 / kOuts waves on it take equal slices of the in_f inputs (so a
+// narrow output still puts work on every CU), and the slices' sums meet in
+// LDS.  acc[r] = W[o, :] . xn[r, :] for r < rows, where xn = x, or with kLN
+// the LayerNorm of each x row (mean and rstd computed by the workgroup: the
+// decode step's rows are at most 8 of a few thousand features).
+template <bool kVec, bool kLN, int kOuts>
+__global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a) {
+    constexpr int kSplit = kWaves / kOuts;
+    __shared__ float part[kWaves][kMaxRows];
+    __shared__ float stat[2][kMaxRows];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int in_f = a.in_f, rows = a.rows;
+    if (kLN) {
+        // Mean and E[x^2] - mean^2 of each row, as layer_norm_forward_cuda_kernel
+        // (and gpt.c's LayerNorm.c) compute them; wave r handles rows r, r+4, ...
+        for (int r = w; r < rows; r += kWaves) {
+            const float *xr = a.x + static_cast<int64_t>(r) * in_f;
+            float s = 0.0f, ss = 0.0f;
+            if (kVec) {  // 16-byte loads, all of a lane's loads issued together
+                constexpr int kU = 4;
+                for (int j0 = lane; j0 < in_f / 4; j0 += kU * kWave) {
+                    f32x4_t v[kU];
+#pragma unroll
+                    for (int u = 0; u < kU; ++u) {
+                        const int j = j0 + u * kWave;
+                        v[u] = j < in_f / 4 ? reinterpret_cast<const f32x4_t *>(xr)[j] : f32x4_t{0, 0, 0, 0};
+                    }
+#pragma unroll
+                    for (int u = 0; u < kU; ++u)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            s += v[u][e];
+                            ss += v[u][e] * v[u][e];
+                        }
+                }
+            } else {
+                for (int j = lane; j < in_f; j += kWave) {
+                    s += xr[j];
+                    ss += xr[j] * xr[j];
+                }
+            }
+            s = wave_sum(s);
+            ss = wave_sum(ss);
+            const float scale = 1.0f / in_f;
+            const float mean = s * scale;
+            const float var = ss * scale - mean * mean;
+            if (lane == 0) {
+                stat[0][r] = mean;
+                stat[1][r] = 1.0f / sqrtf(var + a.eps);
+            }
+        }
+        __syncthreads();
+    }
+    const int o = blockIdx.x * kOuts + w / kSplit;
+    const int slice = w % kSplit;
+    const int per = (in_f + kSplit - 1) / kSplit;
+    const int j0 = slice * per, j1 = min(in_f, j0 + per);
     float acc[kMaxRows];
 #pragma unroll
     for (int r = 0; r < kMaxRows; ++r) acc[r] = 0.0f;
-    if (kVec) {
-        const int n4 = in_f / 4;
-        for (int j = lane; j < n4; j += kWave) {
-            const f32x4_t wv = reinterpret_cast<const f32x4_t *>(w)[j];
+    if (o < a.out_f) {
+        const float *wrow = a.W + static_cast<int64_t>(o) * in_f;
+        if (kVec) {  // in_f % (4 kSplit) == 0: slices are whole 16-byte vectors
+            for (int j = j0 / 4 + lane; j < j1 / 4; j += kWave) {
+                const f32x4_t wv = reinterpret_cast<const f32x4_t *>(wrow)[j];
+                f32x4_t lw = {1.0f, 1.0f, 1.0f, 1.0f}, lb = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (kLN) {
+                    lw = reinterpret_cast<const f32x4_t *>(a.ln_w)[j];
+                    if (a.ln_b != nullptr) lb = reinterpret_cast<const f32x4_t *>(a.ln_b)[j];
+                }
 #pragma unroll
-            for (int r = 0; r < kMaxRows; ++r) {
-                if (r < rows) {
-                    const f32x4_t xv = reinterpret_cast<const f32x4_t *>(x + static_cast<int64_t>(r) * in_f)[j];
-                    acc[r] = fmaf(wv[0], xv[0], acc[r]);
-                    acc[r] = fmaf(wv[1], xv[1], acc[r]);
-                    acc[r] = fmaf(wv[2], xv[2], acc[r]);
-                    acc[r] = fmaf(wv[3], xv[3], acc[r]);
+                for (int r = 0; r < kMaxRows; ++r) {
+                    if (r < rows) {
+                        f32x4_t xv = reinterpret_cast<const f32x4_t *>(a.x + static_cast<int64_t>(r) * in_f)[j];
+                        if (kLN) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) xv[e] = (xv[e] - stat[0][r]) * stat[1][r] * lw[e] + lb[e];
+                        }
+                        acc[r] = fmaf(wv[0], xv[0], acc[r]);
+                        acc[r] = fmaf(wv[1], xv[1], acc[r]);
+                        acc[r] = fmaf(wv[2], xv[2], acc[r]);
+                        acc[r] = fmaf(wv[3], xv[3], acc[r]);
+                    }
+                }
+            }
+        } else {
+            for (int j = j0 + lane; j < j1; j += kWave) {
+                const float wv = wrow[j];
+#pragma unroll
+                for (int r = 0; r < kMaxRows; ++r) {
+                    if (r < rows) {
+                        float xv = a.x[static_cast<int64_t>(r) * in_f + j];
+                        if (kLN)
+                            xv = (xv - stat[0][r]) * stat[1][r] * a.ln_w[j] + (a.ln_b != nullptr ? a.ln_b[j] : 0.0f);
+                        acc[r] = fmaf(wv, xv, acc[r]);
+                    }
                 }
             }
         }
-    } else {
-        for (int j = lane; j < in_f; j += kWave) {
-            const float wv = w[j];
-#pragma unroll
-            for (int r = 0; r < kMaxRows; ++r)
-                if (r < rows) acc[r] = fmaf(wv, x[static_cast<int64_t>(r) * in_f + j], acc[r]);
-        }
     }
 #pragma unroll
-    for (int r = 0; r < kMaxRows; ++r) {
+    for (int r = 0; r < kMaxRows; ++r)
         if (r < rows) {
-            float v = wave_sum(acc[r]);
-            if (lane == 0) {
-                if (b != nullptr) v += b[o];
-                if (act == 1) v = gelu_tanh(v);
-                if (res != nullptr) v += res[static_cast<int64_t>(r) * out_f + o];
-                y[static_cast<int64_t>(r) * out_f + o] = v;
-            }
+            const float v = wave_sum(acc[r]);
+            if (lane == 0) part[w][r] = v;
+        }
+    __syncthreads();
+    // One thread per (output, row) adds the slices in order and finishes.
+    const int t = threadIdx.x;
+    if (t < kOuts * rows) {
+        const int oo = t / rows, r = t % rows;
+        const int out = blockIdx.x * kOuts + oo;
+        if (out < a.out_f) {
+            float v = part[oo * kSplit][r];
+#pragma unroll
+            for (int s = 1; s < kSplit; ++s) v += part[oo * kSplit + s][r];
+            if (a.b != nullptr) v += a.b[out];
+            if (a.act == 1) v = gelu_tanh(v);
+            if (a.res != nullptr) v += a.res[static_cast<int64_t>(r) * a.out_f + out];
+            a.y[static_cast<int64_t>(r) * a.out_f + out] = v;
         }
     }
 }
 
-// out[r, :] = wte[ids[r], :] + wpe[pos, :]; an id outside [0, V) gives NaN.
+template <bool kLN, int kOuts>
+void launch_rows(const RowsArgs &a, bool vec, hipStream_t s) {
+    const dim3 grid((a.out_f + kOuts - 1) / kOuts);
+    if (vec)
+        linear_rows_kernel<true, kLN, kOuts><<<grid, dim3(kThreads), 0, s>>>(a);
+    else
+        linear_rows_kernel<false, kLN, kOuts><<<grid, dim3(kThreads), 0, s>>>(a);
+    hipCheck(hipGetLastError());
+}
+
+// Narrow outputs (under 4096 features) split each dot product over the 4
+// waves of a workgroup; wide ones give each wave its own feature.
+void run_rows(const RowsArgs &a, hipStream_t s) {
+    const bool narrow = a.out_f < 4096;
+    const int split = narrow ? 4 : 1;
+    const bool vec = (a.in_f % (4 * split)) == 0 && aligned16(a.W) && aligned16(a.x) &&
+                     (a.ln_w == nullptr || (aligned16(a.ln_w) && aligned16(a.ln_b)));
+    if (a.ln_w != nullptr) {
+        if (narrow) launch_rows<true, 1>(a, vec, s);
+        else launch_rows<true, 4>(a, vec, s);
+    } else {
+        if (narrow) launch_rows<false, 1>(a, vec, s);
+        else launch_rows<false, 4>(a, vec, s);
+    }
+}
+
+// out[r, :] = wte[id, :] + wpe[pos, :] with id = ids[r * ids_stride + pos]
+// (pos_dev set: the position is *pos_dev) or ids[r] (host position); an id
+// outside [0, V) gives NaN.
 __global__ __launch_bounds__(kThreads) void embed_token_kernel(const float *__restrict__ wte,
                                                               const float *__restrict__ wpe,
                                                               const float *__restrict__ ids, float *__restrict__ out,
-                                                              int C, int V, int pos) {
+                                                              int C, int V, int pos, const int *pos_dev,
+                                                              int ids_stride, int P) {
     const int r = blockIdx.x;
-    const int ix = static_cast<int>(ids[r]);
+    if (pos_dev != nullptr) {
+        pos = *pos_dev;
+        if (pos < 0 || pos >= P) return;  // P: rows of the position table and of the id buffer
+    }
+    const int ix = static_cast<int>(ids[pos_dev != nullptr ? static_cast<int64_t>(r) * ids_stride + pos : r]);
     const bool ok = ix >= 0 && ix < V;
     for (int j = threadIdx.x; j < C; j += kThreads)
         out[static_cast<int64_t>(r) * C + j] =
@@ -97,8 +212,12 @@ constexpr int kArgWaves = kArgThreads / kWave;
 // ids[r] = the first index of the largest value of logits row r (NaN never wins).
 // 1024 threads; each takes 4 strided elements per round with the 4 loads
 // issued together, so a 50257-wide row is about 13 memory round trips.
+// With pos_dev set, the token goes to ids[r * stride + *pos_dev + 1], and only
+// once the prompt (positions < prompt) has been consumed and while it is
+// below total.
 __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__restrict__ logits,
-                                                            float *__restrict__ ids, int V) {
+                                                            float *__restrict__ ids, int V, const int *pos_dev,
+                                                            int stride, int prompt, int total) {
     __shared__ float sv[kArgWaves];
     __shared__ int si[kArgWaves];
     const float *row = logits + static_cast<int64_t>(blockIdx.x) * V;
@@ -139,8 +258,19 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__rest
                 best = sv[i];
                 bi = si[i];
             }
-        ids[blockIdx.x] = static_cast<float>(bi < V ? bi : 0);
+        const float tok = static_cast<float>(bi < V ? bi : 0);
+        if (pos_dev == nullptr) {
+            ids[blockIdx.x] = tok;
+        } else {
+            const int nxt = *pos_dev + 1;
+            if (nxt >= prompt && nxt < total) ids[static_cast<int64_t>(blockIdx.x) * stride + nxt] = tok;
+        }
     }
+}
+
+// The step's last node: the next position.
+__global__ void advance_pos_kernel(int *pos_dev) {
+    if (threadIdx.x == 0) *pos_dev += 1;
 }
 
 }  // namespace
@@ -151,6 +281,11 @@ using namespace gptc;
 
 extern "C" void gptc_linear_rows_cuda(const tensor_t *W, const tensor_t *b, const tensor_t *x,
                                       const tensor_t *residual, const int act, tensor_t *y) {
+    gptc::ln_linear_rows(nullptr, nullptr, 0.0f, W, b, x, residual, act, y);
+}
+
+void gptc::ln_linear_rows(const tensor_t *ln_w, const tensor_t *ln_b, float eps, const tensor_t *W, const tensor_t *b,
+                          const tensor_t *x, const tensor_t *residual, int act, tensor_t *y) {
     check_gpu(W, "W");
     check_gpu(x, "x");
     check_gpu(y, "y");
@@ -169,16 +304,25 @@ extern "C" void gptc_linear_rows_cuda(const tensor_t *W, const tensor_t *b, cons
         check_gpu(residual, "residual");
         CHECK_ERROR(residual->length != y->length, "Expected the residual to match y's %d elements.", y->length);
     }
-    const bool vec = (in_f % 4) == 0 && aligned16(W->t) && aligned16(x->t);
-    const dim3 grid((out_f + kWaves - 1) / kWaves);
-    hipStream_t s = gptc_stream_checked();
-    const float *bp = b != NULL ? b->t : nullptr;
-    const float *rp = residual != NULL ? residual->t : nullptr;
-    if (vec)
-        linear_rows_kernel<true><<<grid, dim3(kThreads), 0, s>>>(W->t, bp, x->t, rp, y->t, rows, in_f, out_f, act);
-    else
-        linear_rows_kernel<false><<<grid, dim3(kThreads), 0, s>>>(W->t, bp, x->t, rp, y->t, rows, in_f, out_f, act);
-    hipCheck(hipGetLastError());
+    if (ln_w != nullptr) {
+        check_gpu(ln_w, "ln_w");
+        CHECK_ERROR(ln_w->length != in_f || (ln_b != nullptr && ln_b->length != in_f),
+                    "Expected the LayerNorm parameters to hold %d elements.", in_f);
+    }
+    RowsArgs a;
+    a.W = W->t;
+    a.b = b != NULL ? b->t : nullptr;
+    a.x = x->t;
+    a.res = residual != NULL ? residual->t : nullptr;
+    a.y = y->t;
+    a.ln_w = ln_w != nullptr ? ln_w->t : nullptr;
+    a.ln_b = ln_w != nullptr && ln_b != nullptr ? ln_b->t : nullptr;
+    a.eps = eps;
+    a.rows = rows;
+    a.in_f = in_f;
+    a.out_f = out_f;
+    a.act = act;
+    run_rows(a, gptc_stream_checked());
 }
 
 extern "C" void gptc_embed_token_cuda(const tensor_t *wte, const tensor_t *wpe, const tensor_t *ids, const int pos,
@@ -192,8 +336,8 @@ extern "C" void gptc_embed_token_cuda(const tensor_t *wte, const tensor_t *wpe, 
     CHECK_ERROR(pos < 0 || pos >= wpe->shape[0], "Expected 0 <= pos < %d, but got pos = %d.", wpe->shape[0], pos);
     CHECK_ERROR(out->length != ids->length * C, "Expected out to hold %d x %d elements.", ids->length, C);
     if (ids->length == 0) return;
-    embed_token_kernel<<<dim3(ids->length), dim3(kThreads), 0, gptc_stream_checked()>>>(wte->t, wpe->t, ids->t,
-                                                                                        out->t, C, V, pos);
+    embed_token_kernel<<<dim3(ids->length), dim3(kThreads), 0, gptc_stream_checked()>>>(
+        wte->t, wpe->t, ids->t, out->t, C, V, pos, nullptr, 1, wpe->shape[0]);
     hipCheck(hipGetLastError());
 }
 
@@ -203,6 +347,31 @@ extern "C" void gptc_argmax_cuda(const tensor_t *logits, tensor_t *ids) {
     const int V = last_dim(logits), rows = leading_rows(logits);
     CHECK_ERROR(ids->length != rows, "Expected %d ids, but got %d.", rows, ids->length);
     if (rows == 0) return;
-    argmax_kernel<<<dim3(rows), dim3(kArgThreads), 0, gptc_stream_checked()>>>(logits->t, ids->t, V);
+    argmax_kernel<<<dim3(rows), dim3(kArgThreads), 0, gptc_stream_checked()>>>(logits->t, ids->t, V, nullptr, 1, 0,
+                                                                                 0);
+    hipCheck(hipGetLastError());
+}
+
+// ---- the device-position forms used by the captured generation step ----
+
+void gptc::launch_embed_tokens_devpos(const tensor_t *wte, const tensor_t *wpe, const float *tokens, int B,
+                                      int stride, const int *pos_dev, tensor_t *out) {
+    const int V = wte->shape[0], C = wte->shape[1];
+    const int limit = stride < wpe->shape[0] ? stride : wpe->shape[0];
+    embed_token_kernel<<<dim3(B), dim3(kThreads), 0, gptc_stream_checked()>>>(wte->t, wpe->t, tokens, out->t, C, V,
+                                                                              0, pos_dev, stride, limit);
+    hipCheck(hipGetLastError());
+}
+
+void gptc::launch_argmax_next(const tensor_t *logits, float *tokens, int stride, const int *pos_dev, int prompt,
+                              int total) {
+    const int V = last_dim(logits), rows = leading_rows(logits);
+    argmax_kernel<<<dim3(rows), dim3(kArgThreads), 0, gptc_stream_checked()>>>(logits->t, tokens, V, pos_dev, stride,
+                                                                                 prompt, total);
+    hipCheck(hipGetLastError());
+}
+
+void gptc::launch_advance_pos(int *pos_dev) {
+    advance_pos_kernel<<<dim3(1), dim3(64), 0, gptc_stream_checked()>>>(pos_dev);
     hipCheck(hipGetLastError());
 }

@@ -54,6 +54,27 @@ def window_generate(rt, model, prompt, total, block_size, keep_logits=False):
     return X[:total].astype(np.int64), rows
 
 
+def graph_generate(rt, model, prompt, total, cache=None):
+    """gptc_gpt2_generate: the whole greedy loop on the GPU (one captured step
+    replayed per position), for one or more prompts of equal length.
+    prompt: (P,) or (B, P) ids.  Returns the (B, total) or (total,) tokens."""
+    p = np.asarray(prompt)
+    single = p.ndim == 1
+    p = p.reshape(1, -1) if single else p
+    B, P = p.shape
+    buf = np.zeros((B, total), np.float32)
+    buf[:, :P] = p
+    tokens = rt.from_numpy(buf)
+    own = cache is None
+    cache = cache or gptc.KVCache(rt, model, B, total)
+    rt.lib.gptc_gpt2_generate(model.raw, cache.raw, tokens, P, total)
+    out = rt.to_numpy(tokens).astype(np.int64)
+    rt.free(tokens)
+    if own:
+        cache.free()
+    return out[0] if single else out
+
+
 def kv_generate(rt, model, prompt, total, block_size, keep_logits=False):
     lib = rt.lib
     cache = gptc.KVCache(rt, model, 1, total)

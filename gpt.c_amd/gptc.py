@@ -171,6 +171,7 @@ SIGNATURES = {
     "gptc_kv_cache_create": (_vp, [_vp, _ci, _ci]),
     "gptc_kv_cache_free": (None, [_vp]),
     "gptc_gpt2_decode": (TensorP, [_vp, _vp, TensorP, _ci]),
+    "gptc_gpt2_generate": (None, [_vp, _vp, TensorP, _ci, _ci]),
     # tensor.h (BLAS front ends)
     "saxpy": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),
     "sgemm": (None, [_ci, _ci, _ci, _ci, _ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci, _cf, TensorP, _ci, _ci]),

@@ -7,15 +7,27 @@
  * same logits while reading each weight and cached row once per token.
  *
  * gptc_kv_cache_create(gpt, B, L)   per-layer K and V caches (B, H, L, D) on
- *                                   the GPU for B sequences of up to L tokens.
+ *                                   the GPU for B <= 8 sequences of up to
+ *                                   L <= block_size tokens, and the step's
+ *                                   activations.
  * gptc_gpt2_decode(gpt, kv, ids, pos)
  *                                   ids (B, 1) token ids (floats, GPU) at
  *                                   position pos of every sequence; returns
- *                                   the logits (B, 1, V) of that position and
- *                                   stores the token's keys and values at pos.
- *                                   Positions 0 .. pos-1 must have been
- *                                   decoded before (prefill = decode them in
- *                                   order).  B <= 8, pos < L <= block_size.
+ *                                   the logits (B, 1, V) of that position (a
+ *                                   new tensor) and stores the token's keys
+ *                                   and values at pos.  Positions 0 .. pos-1
+ *                                   must have been decoded before.
+ * gptc_gpt2_generate(gpt, kv, tokens, prompt, total)
+ *                                   greedy generation on the GPU: tokens is a
+ *                                   (B, total) float buffer holding each
+ *                                   sequence's prompt in columns 0 .. prompt-1;
+ *                                   columns prompt .. total-1 receive the
+ *                                   argmax tokens.  One step (positions 0 ..
+ *                                   total-2) is captured once as a HIP graph
+ *                                   and replayed, the position living in
+ *                                   device memory, so the host does not wait
+ *                                   between tokens.  Returns without
+ *                                   synchronising; total <= L.
  * gptc_kv_cache_free(kv)
  */
 #pragma once
@@ -31,14 +43,21 @@ typedef struct gptc_kv_cache {
     int n_layers;
     int B;
     int L;
-    tensor_t **k;  // n_layers tensors (B, H, L, D)
+    tensor_t **k;          // n_layers tensors (B, H, L, D)
     tensor_t **v;
     tensor_t *scratch[8];  // activations of one step, reused across steps
+    tensor_t *logits;      // (B, 1, V) of the captured step
+    int *pos_dev;          // device-side position of the captured step
+    void *graph_exec;      // hipGraphExec_t of the captured step
+    const float *graph_tokens;
+    int graph_prompt;
+    int graph_total;
 } gptc_kv_cache_t;
 
 gptc_kv_cache_t *gptc_kv_cache_create(const gpt2_t *gpt, const int B, const int L);
 void gptc_kv_cache_free(gptc_kv_cache_t *kv);
 tensor_t *gptc_gpt2_decode(gpt2_t *gpt, gptc_kv_cache_t *kv, const tensor_t *ids, const int pos);
+void gptc_gpt2_generate(gpt2_t *gpt, gptc_kv_cache_t *kv, tensor_t *tokens, const int prompt, const int total);
 
 #ifdef __cplusplus
 }
