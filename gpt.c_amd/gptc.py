@@ -90,6 +90,19 @@ SIGNATURES = {
     "check_error": (None, [ctypes.c_bool, ctypes.c_char_p, _ci, ctypes.c_char_p]),
     "malloc_check": (_vp, [ctypes.c_size_t, ctypes.c_char_p, _ci]),
     "aligned_malloc_check": (_vp, [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_char_p, _ci]),
+    "fopen_check": (_vp, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _ci]),
+    "fread_check": (None, [_vp, ctypes.c_size_t, ctypes.c_size_t, _vp, ctypes.c_char_p, _ci]),
+    "fclose_check": (None, [_vp, ctypes.c_char_p, _ci]),
+    "fseek_check": (None, [_vp, ctypes.c_long, _ci, ctypes.c_char_p, _ci]),
+    "print_table": (None, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p), ctypes.c_size_t]),
+    "tensor_check": (None, [TensorP, ctypes.c_char_p, _ci]),
+    "tensor_device_check": (None, [TensorP, TensorP, ctypes.c_char_p, _ci]),
+    # dataloader.h, tokenizer.h, checkpoint.h
+    "DataLoader": (_vp, [ctypes.c_char_p, _ci, _ci]),
+    "Tokenizer": (_vp, [ctypes.c_char_p]),
+    "safe_printf": (None, [ctypes.c_char_p]),
+    "gptc_load_model": (_vp, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_size_t)]),
+    "gptc_save_model": (None, [ctypes.c_char_p, _vp, ctypes.c_size_t]),
     # attention.h
     "Attention": (AttentionP, [_ci, _ci, _ci]),
     # dispatch.h
@@ -441,6 +454,19 @@ class GPT2Model(_Layer):
     def __init__(self, rt, block_size, vocab_size, n_layers, n_heads, n_embd):
         self.cfg = GPT2Config(block_size, vocab_size, n_layers, n_heads, n_embd)
         super().__init__(rt, rt.lib.GPT2(ctypes.byref(self.cfg)), GPT2T)
+
+    @classmethod
+    def from_checkpoint(cls, rt, path):
+        """gptc_load_model(path): a GPT2 on the CPU; returns (model, steps)."""
+        steps = ctypes.c_size_t()
+        raw = rt.lib.gptc_load_model(os.fsencode(path), ctypes.byref(steps))
+        model = cls.__new__(cls)
+        _Layer.__init__(model, rt, raw, GPT2T)
+        return model, steps.value
+
+    def save(self, path, steps=0):
+        """gptc_save_model(path, model, steps)."""
+        self.rt.lib.gptc_save_model(os.fsencode(path), self.raw, steps)
 
     def fast_load(self, arrays):
         """fast_load_state_dict from numpy arrays in parameters() order."""
