@@ -12,6 +12,7 @@
 #include "embedding.h"
 #include "layer_norm.h"
 #include "linear.h"
+#include "loss.h"
 #include "tensor.h"
 
 #ifdef __cplusplus

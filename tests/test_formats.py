@@ -8,8 +8,9 @@ numpy writer/reader that restates the reference's Python tooling:
                  src/dataloader.c:14-101;
   * tokenizer    tokenizer.py:12-40 (header, then length byte + bytes) read by
                  src/tokenizer.c:16-114.
-A file written by numpy loads into the same parameters / batches / strings;
-a file the library writes is byte-identical to numpy's.  The GPU case (saving
+(the writers are in file_formats.py).  A file written by numpy loads into the
+same parameters / batches / strings; a file the library writes is
+byte-identical to numpy's.  The GPU case (saving
 a model whose parameters live on the device) is in test_gpt2_gpu.py's style
 at the end, marked gpu.
 """
@@ -23,6 +24,7 @@ import numpy as np
 import pytest
 
 import gptc
+from file_formats import write_checkpoint, write_tokenizer
 from gpt2_oracle import param_shapes
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -48,30 +50,13 @@ def rt():
     return gptc.Runtime(gptc.load())
 
 
-def numpy_write_checkpoint(path, cfg, params, step):
-    """model.py's write_model: int32 header[256], shape words, float32 data."""
-    block, V, L, H, C = cfg
-    header = np.zeros(256, np.int32)
-    header[:6] = [20240415, block, V, L, H, C]
-    shapes = []
-    for p in params:
-        shapes += [p.ndim] + list(p.shape)
-    header[6] = len(shapes)
-    header[7] = step
-    with open(path, "wb") as f:
-        f.write(header.tobytes())
-        f.write(np.array(shapes, np.int32).tobytes())
-        for p in params:
-            f.write(np.ascontiguousarray(p, np.float32).tobytes())
-
-
 def test_checkpoint_numpy_file_loads_and_saves_identically(rt, tmp_path):
     cfg = (16, 37, 2, 2, 8)  # block, V, layers, heads, C
     block, V, L, H, C = cfg
     rng = np.random.default_rng(0)
     params = [rng.standard_normal(shp).astype(np.float32) for _, shp in param_shapes(V, block, L, C)]
     src = tmp_path / "model.bin"
-    numpy_write_checkpoint(src, cfg, params, step=123)
+    write_checkpoint(src, cfg, params, step=123)
     model, steps = gptc.GPT2Model.from_checkpoint(rt, src)
     assert steps == 123
     s = model.s
@@ -125,20 +110,10 @@ def test_dataloader_windows_targets_and_wraparound(rt, tmp_path):
     ctypes.CFUNCTYPE(None, ctypes.c_void_p)(dl.free_layer)(raw)
 
 
-def numpy_write_tokenizer(path, pieces, eot):
-    """tokenizer.py's write_tokenizer."""
-    header = np.zeros(256, np.int32)
-    header[:3] = [20240415, len(pieces), eot]
-    with open(path, "wb") as f:
-        f.write(header.tobytes())
-        for b in pieces:
-            f.write(bytes([len(b)]) + b)
-
-
 def test_tokenizer_decodes(rt, tmp_path):
     pieces = [b"Hello", b",", b" world", b"\xe2\x82\xac", b"!", b"<|endoftext|>", bytes(range(1, 256))[:255]]
     path = tmp_path / "tokenizer.bin"
-    numpy_write_tokenizer(path, pieces, eot=5)
+    write_tokenizer(path, pieces, eot=5)
     raw = rt.lib.Tokenizer(os.fsencode(path))
     tk = ctypes.cast(raw, ctypes.POINTER(TokenizerT)).contents
     assert tk.vocab_size == len(pieces) and tk.eot_token == 5
@@ -173,5 +148,5 @@ def test_checkpoint_saved_from_gpu_round_trips(tmp_path):
     model.save(path, steps=7)
     model.free()
     ref = tmp_path / "ref.bin"
-    numpy_write_checkpoint(ref, (block, V, L, H, C), params, step=7)
+    write_checkpoint(ref, (block, V, L, H, C), params, step=7)
     assert open(path, "rb").read() == open(ref, "rb").read()
