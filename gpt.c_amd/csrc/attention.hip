@@ -206,7 +206,7 @@ extern "C" void attention_forward_cuda_kernel(const tensor_t *input, const tenso
     p.bh_pad = bh_padded(d.B * d.H);
     p.vec = (d.D % 4 == 0) && aligned16(input->t) && aligned16(output->t) && aligned16(p.o2) &&
             (!p.qp || (aligned16(p.qp) && aligned16(p.kp) && aligned16(p.vp)));
-    p.full = p.vec && full_tiles(d, {p.k.st, p.v.st});
+    p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.v.st});
     gptc::launch_attn_fwd(p, gptc_stream_checked(), g_have_events ? g_events : nullptr);
 }
 

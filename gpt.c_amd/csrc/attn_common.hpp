@@ -41,6 +41,17 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x4_f32 (wave64), the shape of the 16-row kernels:
+//   A (16 x 4):  lane l holds A[l % 16][l / 16]
+//   B (4 x 16):  lane l holds B[l / 16][l % 16]
+//   D (16 x 16): lane l, register r holds D[4*(l/16) + r][l % 16]
+// Register r of a product, across the wave, is again a B operand whose
+// reduction rows are 4g + r (g = l / 16): accumulators feed the next product
+// without a shuffle, as with the 32 x 32 shape.
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
     f32x16 z;
 #pragma unroll
@@ -113,5 +124,24 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 // Value held by the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32, 64); }
+
+// Max and sum over the four lanes l % 16 + {0, 16, 32, 48} (one query of a
+// 16 x 16 accumulator), every lane receiving the result.  gfx950's
+// v_permlane32_swap / v_permlane16_swap exchange lane halves / 16-lane rows
+// in the VALU: with both operands equal to x, the two results hold x at the
+// lane and at its partner (l ^ 32, then l ^ 16), in some order.
+__device__ __forceinline__ float max4_rows(float x) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float sum4_rows(float x) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 }  // namespace gptc

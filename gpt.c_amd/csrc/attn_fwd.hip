@@ -7,14 +7,20 @@
 // (kernels/src/cuda/Attention.cu:170-232; math of
 // kernels/src/cpu/Attention.c:46-167).
 //
-// One workgroup = 4 waves = 128 queries of one (b, h); wave w owns 32
-// queries.  The products are formed transposed, S^T = K Q^T and
+// Two kernels.  For D == 64 with 16-byte rows (every GPT-2 shape) the
+// 16-row kernel at the end of this file runs; the 32-row kernel first below
+// serves the other head sizes.
+//
+// 32-row kernel: one workgroup = 4 waves = 128 queries of one (b, h); wave
+// w owns 32 queries.  The products are formed transposed, S^T = K Q^T and
 // O^T = V^T P^T, so that each lane owns ONE query (lane % 32) and the
 // softmax row statistics are per-lane scalars: the running max needs one
 // exchange with the other wave half per 64-key tile, the running sum none
 // until the epilogue.  Q stays in registers as the B operand; 64-key K and
 // V tiles are staged in LDS by the whole workgroup and prefetched into
 // registers one tile ahead.
+#include <type_traits>
+
 #include "attn_common.hpp"
 #include "attn_kernels.hpp"
 #include "hip_check.hpp"
@@ -233,9 +239,238 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     if (hf == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(l_tot)) * kLn2;
 }
 
+// ---- The 16-row forward (D == 64, buffer-resource loads): paired blocks ----
+//
+// One workgroup = 4 waves = one 64-query block j of one (b, h) and then the
+// block nqt-1-j of the same head.  A block j needs key tiles 0 .. j, so every
+// pair costs nqt + 1 tiles: all workgroups of the grid get the same work and
+// are resident together (with one block per workgroup the long blocks run
+// on, with their CUs half empty, after the short ones are done).
+// Wave w owns queries 16w .. 16w+15 of the block; lane (g = lane/16,
+// i = lane%16) owns query i of them and, of every 16-key block, keys
+// 4g .. 4g+3 (the 16 x 16 x 4 accumulator layout of attn_common.hpp).  The
+// products are formed transposed as in the kernel above: S^T = K Q^T with
+// Q^T in registers, O^T = V^T P^T with P^T straight from the S accumulators.
+// Output row m of O^T block db is dim 4m + db, so that one 16-byte LDS read
+// of a V row gives a lane the A operands of all four blocks.  P' and m go
+// out in the same packed layout, so the backward is unchanged.
+constexpr int kF16Rows = 64;  // queries per block of the 16-row kernel (4 waves x 16)
+
+template <int N>
+using IntC = std::integral_constant<int, N>;
+
+template <bool PERM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_fwd16_kernel(const FwdParams a) {
+    __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
+
+    // All pairs of a head on one XCD (blockIdx % 8), so its K and V stay in
+    // that XCD's L2.
+    const int nbh_x = a.bh_pad / kXcds;
+    const int idx = blockIdx.x / kXcds;
+    const int pair = idx / nbh_x;
+    const int bh = blockIdx.x % kXcds + kXcds * (idx - pair * nbh_x);
+    if (bh >= a.B * a.H) return;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int T = a.T, nqt = a.nqt;
+    const int jA = pair, jB = nqt - 1 - pair;  // jB == jA: the middle block of an odd nqt, alone
+    const int nA = jA + 1;
+    const int n_steps = nA + (jB != jA ? jB + 1 : 0);
+
+    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
+    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
+    const auto q_rows = head_rows(Qh, T, a.q.st);
+    const auto k_rows = head_rows(Kh, T, a.k.st);
+    const auto v_rows = head_rows(Vh, T, a.v.st);
+
+    // Cooperative tile load: thread covers rows (tid>>4) + 16i, dims 4*(tid&15).
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    f32x4 kpre[4], vpre[4];
+    auto prefetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t key = kt * kFwdBN + ld_row + 16 * i;
+            kpre[i] = buffer_load4(k_rows, key * a.k.st + ld_col);
+            vpre[i] = buffer_load4(v_rows, key * a.v.st + ld_col);
+        }
+    };
+    prefetch(0);
+
+    const float c2 = a.scale_log2;
+    f32x4 qr[4];  // Q[my_q][16g + 4c + e] in qr[c][e]: the B operand of step 4c + e
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4 acc[4];  // O^T: acc[db][r] = O[my_q][16g + 4r + db] before the 1/l scaling
+    int jq = jA, kt = 0, my_q = 0;
+
+    // One key tile for this wave: NKB 16-key blocks of it are visible to the
+    // wave's queries (DIAG: the tile holding the block's own keys, where block
+    // NKB - 1 is masked per key and blocks NKB .. 3 are all masked).
+    auto tile = [&](auto nkb_c, auto diag_c) {
+        constexpr int NKB = decltype(nkb_c)::value;
+        constexpr bool DIAG = decltype(diag_c)::value;
+
+        f32x4 sc[4];  // S^T: sc[kb][r] = S[my_q][16kb + 4g + r]
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) sc[kb] = zero4();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            f32x4 ka[NKB];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+                ka[kb] = *reinterpret_cast<const f32x4 *>(&k_lds[(16 * kb + i16) * kLdsStride + 16 * g + 4 * c]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) sc[kb] = mfma16(ka[kb][e], qr[c][e], sc[kb]);
+        }
+        if (DIAG) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * g + r > i16) sc[NKB - 1][r] = -INFINITY;
+        }
+
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+            mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
+        const float mt = max4_rows(mx) * c2;
+
+        // Lazy rescaling, as in the kernel above.
+        if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleLog2) != 0) {
+            const float m_new = fmaxf(m_run, mt);
+            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+            const float alpha = fast_exp2(m_run - m_use);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+            m_run = m_new;
+        }
+        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        float ls[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = fast_exp2(fmaf(sc[kb][r], c2, -m_use));
+                sc[kb][r] = p;
+                ls[r & 1] += p;
+            }
+        l_run += ls[0] + ls[1];
+
+        // P' rows of block (jq, key blocks 2kt and 2kt + 1), zeros past the
+        // diagonal; m of this tile.
+        {
+            float *ptile = a.pp + ds_block_offset(bh, nqt, jq, 2 * kt);  // uniform
+            const uint32_t prow = (16 * w + i16) * 32 + 4 * g;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                *reinterpret_cast<f32x4 *>(ptile + (kb >> 1) * kDsBlock + prow + 16 * (kb & 1)) =
+                    kb < NKB ? sc[kb] : zero4();
+            if (g == 0 && my_q < T) a.pm[(static_cast<uint32_t>(bh) * nqt + kt) * T + my_q] = m_use;
+        }
+
+        // O^T += V^T P^T: step (kb, r) reduces keys 16kb + 4g' + r; lane i's
+        // A operands for the four dim blocks are V[key][4i .. 4i+3].
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const f32x4 va = *reinterpret_cast<const f32x4 *>(&v_lds[(16 * kb + 4 * g + r) * kLdsStride + 4 * i16]);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) acc[db] = mfma16(va[db], sc[kb][r], acc[db]);
+            }
+    };
+
+    for (int s = 0; s < n_steps; ++s) {
+        const bool second = s >= nA;
+        jq = second ? jB : jA;     // query block
+        kt = second ? s - nA : s;  // key tile
+        my_q = jq * kF16Rows + 16 * w + i16;
+        if (kt == 0) {
+            // A new block: its Q rows (rows past T read as zeros) and fresh statistics.
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(my_q) * a.q.st + 16 * g + 4 * c);
+            if (PERM && my_q < T) {
+                float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * kDPad + 16 * g;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) *reinterpret_cast<f32x4 *>(dst + 4 * c) = qr[c];
+            }
+            m_run = -INFINITY;
+            l_run = 0.0f;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] = zero4();
+        }
+
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ld_row + 16 * i;
+            *reinterpret_cast<f32x4 *>(&k_lds[row * kLdsStride + ld_col]) = kpre[i];
+            *reinterpret_cast<f32x4 *>(&v_lds[row * kLdsStride + ld_col]) = vpre[i];
+        }
+        const bool diag = kt == jq;  // the block's own keys: the last tile of the block
+        if (PERM && diag) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt * kFwdBN + ld_row + 16 * i;
+                if (key < T) {
+                    const uint32_t off = (static_cast<uint32_t>(bh) * T + key) * kDPad + ld_col;
+                    *reinterpret_cast<f32x4 *>(a.kp + off) = kpre[i];
+                    *reinterpret_cast<f32x4 *>(a.vp + off) = vpre[i];
+                }
+            }
+        }
+        __syncthreads();
+        if (s + 1 < n_steps) prefetch(s + 1 < nA ? s + 1 : s + 1 - nA);
+
+        if (!diag) {
+            tile(IntC<4>{}, std::false_type{});
+            continue;
+        }
+        switch (w) {  // wave-uniform
+            case 0: tile(IntC<1>{}, std::true_type{}); break;
+            case 1: tile(IntC<2>{}, std::true_type{}); break;
+            case 2: tile(IntC<3>{}, std::true_type{}); break;
+            default: tile(IntC<4>{}, std::true_type{}); break;
+        }
+
+        // End of the block: y = O / l and the log-sum-exp.
+        const float lt = sum4_rows(l_run);
+        if (my_q < T) {
+            const float inv = 1.0f / lt;
+            float *orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g;
+            float *o2row = a.o2 ? a.o2 + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g : nullptr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const f32x4 val = {acc[0][r] * inv, acc[1][r] * inv, acc[2][r] * inv, acc[3][r] * inv};
+                *reinterpret_cast<f32x4 *>(orow + 4 * r) = val;
+                if (o2row) *reinterpret_cast<f32x4 *>(o2row + 4 * r) = val;
+            }
+            if (g == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(lt)) * kLn2;
+        }
+    }
+}
+
 void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     FwdParams p = p_in;
     const bool perm = p.qp != nullptr;
+    if (p.full) {
+        const dim3 grid(((p.nqt + 1) / 2) * p.bh_pad), block(256);
+        if (ev) hipCheck(hipEventRecord(ev[0], stream));
+        if (perm)
+            attn_fwd16_kernel<true><<<grid, block, 0, stream>>>(p);
+        else
+            attn_fwd16_kernel<false><<<grid, block, 0, stream>>>(p);
+        hipCheck(hipGetLastError());
+        if (ev) hipCheck(hipEventRecord(ev[1], stream));
+        return;
+    }
     if (p.full && perm)
         p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, true, true>);
     else if (p.full)

@@ -118,6 +118,12 @@ def test_c5_fwd_bwd_b4_t1024_h25(rt, oracle):
     compare_with_oracle(rt, oracle, 4, 1024, 1600, 25, sample_heads=[(0, 0), (2, 13), (3, 24)])
 
 
+def test_odd_block_count_wide_grid(rt, oracle):
+    """T = 960: 15 query blocks of 64, so one block of each head has no
+    partner, on a grid large enough for the three-sub-group workgroups."""
+    compare_with_oracle(rt, oracle, 8, 960, 768, 12, sample_heads=[(0, 0), (5, 6), (7, 11)])
+
+
 def test_reference_cache_layout(rt, oracle):
     """gpt.c's unchanged attention.c allocates q, k, v (B,H,T,D) and att (B,H,T,T)
     caches (attention.c:105-120) and passes a zeroed dout: the entry points
