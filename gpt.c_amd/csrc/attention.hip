@@ -293,11 +293,11 @@ extern "C" long long gptc_attention_state_floats(int B, int T, int C, int n_head
 
 namespace {
 
-// Shape checks and launch of the decode step; the position comes from the
-// host (pos, checked here) or from device memory (pos_dev, checked by the
-// kernel, for graph replays).
-void decode_step(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos, const int *pos_dev,
-                 const int n_heads, tensor_t *output) {
+// Shape checks and launch parameters of the decode step; the position comes
+// from the host (pos, checked here) or from device memory (pos_dev, checked
+// by the kernel, for graph replays).
+gptc::DecParams decode_params(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos,
+                              const int *pos_dev, const int n_heads, tensor_t *output) {
     CHECK_ERROR(qkv == NULL || k_cache == NULL || v_cache == NULL || output == NULL,
                 "Expected qkv, k_cache, v_cache and output to be non-NULL.");
     CHECK_ERROR(qkv->ndims != 3 || qkv->shape[1] != 1 || qkv->shape[2] % 3 != 0,
@@ -326,7 +326,6 @@ void decode_step(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, cons
     }
     CHECK_ERROR(output->length != d.B * d.C, "Expected output of B*C = %d elements, but got %d.", d.B * d.C,
                 output->length);
-    if (d.B == 0 || d.C == 0) return;
 
     gptc::DecParams p{};
     p.qkv = qkv->t;
@@ -342,17 +341,44 @@ void decode_step(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, cons
     p.pos_dev = pos_dev;
     p.scale_log2 = gptc::kLog2e / std::sqrt(static_cast<float>(d.D));
     p.full = d.D == gptc::kDPad && aligned16(k_cache->t) && aligned16(v_cache->t);
+    // Split-key kernels for D == 64: chunks of the keys 0 .. pos, or of the
+    // cache length with a device-side position.
+    if (p.full) p.splits = ((pos_dev == nullptr ? pos + 1 : L) + gptc::kDecChunk - 1) / gptc::kDecChunk;
+    return p;
+}
+
+void decode_step(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos, const int *pos_dev,
+                 const int n_heads, tensor_t *output, float *part) {
+    gptc::DecParams p = decode_params(qkv, k_cache, v_cache, pos, pos_dev, n_heads, output);
+    if (p.B == 0 || p.C == 0) return;
+    // The eager form takes the partials buffer from the stream-ordered
+    // allocator; the merge kernel reads it before anything queued later can
+    // reuse it.
+    bool own_part = false;
+    if (p.full) {
+        if (part == nullptr) {
+            part = static_cast<float *>(
+                alloc_cuda(static_cast<size_t>(p.B) * p.H * p.splits * gptc::kDecPartStride * sizeof(float)));
+            own_part = true;
+        }
+        p.part = part;
+    }
     gptc::launch_attn_decode(p, gptc_stream_checked());
+    if (own_part) free_cuda(part);
 }
 
 }  // namespace
 
 extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos,
                                              const int n_heads, tensor_t *output) {
-    decode_step(qkv, k_cache, v_cache, pos, nullptr, n_heads, output);
+    decode_step(qkv, k_cache, v_cache, pos, nullptr, n_heads, output, nullptr);
 }
 
 void gptc::attention_decode_devpos(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int *pos_dev,
-                                   const int n_heads, tensor_t *output) {
-    decode_step(qkv, k_cache, v_cache, 0, pos_dev, n_heads, output);
+                                   const int n_heads, tensor_t *output, float *part) {
+    decode_step(qkv, k_cache, v_cache, 0, pos_dev, n_heads, output, part);
+}
+
+size_t gptc::attention_decode_part_floats(const int B, const int H, const int L) {
+    return gptc::dec_part_floats(B, H, L);
 }

@@ -10,8 +10,10 @@
 // softmax(q k^T / sqrt(D)) v), reading each cached key and value once.
 //
 // The work is HBM- and latency-bound (4 L D flop against 8 L D bytes per
-// (b, h)): one 1024-thread workgroup (16 waves) per (b, h), with as many row
-// loads in flight as the registers allow.
+// (b, h)).  For D == 64 with 16-byte cache rows the split-key kernels at the
+// end of this file run; the kernel first below serves the other head sizes:
+// one 1024-thread workgroup (16 waves) per (b, h), with as many row loads in
+// flight as the registers allow.
 //   phase 1  thread per key: t_j = (q . k_j) log2(e)/sqrt(D) into LDS;
 //   phase 2  workgroup max m and sum l of p_j = exp2(t_j - m);
 //   phase 3  wave per key row, lane per dim: o = sum_j p_j v_j (coalesced
@@ -149,7 +151,139 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
     }
 }
 
+// ---- Split-key decode (D == 64, 16-byte rows) ----
+//
+// At B = 1 the kernel above runs one workgroup per head, and each of its
+// phases waits for a dependent round trip to HBM; twelve heads leave most of
+// the GPU idle.  Here the keys 0 .. pos of every (b, h) are cut into chunks
+// of kDecChunk, one 256-thread workgroup each, which writes the chunk's
+// partial softmax state (max m_s and sum l_s of exp2(t - m_s), unnormalised
+// o_s = sum p v); a second kernel merges the chunks of each (b, h):
+//   M = max m_s,  l = sum l_s exp2(m_s - M),  o = sum o_s exp2(m_s - M) / l.
+// The workgroup holding key pos takes the new k, v from the qkv row and
+// writes them into the caches at pos; the others read cache rows below pos.
+__global__ __launch_bounds__(256) void attn_decode_split_kernel(const DecParams a) {
+    __shared__ __attribute__((aligned(16))) float q_s[kDPad];
+    __shared__ __attribute__((aligned(16))) float k_s[kDPad];
+    __shared__ __attribute__((aligned(16))) float v_s[kDPad];
+    __shared__ float p_s[kDecChunk];
+    __shared__ float o_red[4][kDPad];
+    __shared__ float red[4];
+
+    const int pos = a.pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*a.pos_dev) : a.pos;
+    if (pos < 0 || pos >= a.L) return;
+    const int bh = blockIdx.x / a.splits, sp = blockIdx.x - bh * a.splits;
+    const int j0 = sp * kDecChunk;
+    if (j0 > pos) return;  // a chunk past the position (fixed grids of graph replays)
+    const int n = min(kDecChunk, pos + 1 - j0);
+    const bool has_pos = pos < j0 + kDecChunk;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    const float *row = a.qkv + static_cast<size_t>(b) * 3 * a.C + h * kDPad;
+    float *kc = a.k_cache + static_cast<size_t>(bh) * a.L * kDPad;
+    float *vc = a.v_cache + static_cast<size_t>(bh) * a.L * kDPad;
+    if (tid < kDPad) {
+        q_s[tid] = row[tid];
+        if (has_pos) {
+            const float kn = row[a.C + tid], vn = row[2 * a.C + tid];
+            k_s[tid] = kn;
+            v_s[tid] = vn;
+            kc[static_cast<size_t>(pos) * kDPad + tid] = kn;
+            vc[static_cast<size_t>(pos) * kDPad + tid] = vn;
+        }
+    }
+    __syncthreads();
+
+    // Scores: four threads per key, 16 dims each.
+    const int kk = tid >> 2, qq = tid & 3;
+    float t = -INFINITY;
+    {
+        float acc = 0.0f;
+        if (kk < n) {
+            const int j = j0 + kk;
+            const float *kr = (j == pos) ? k_s : kc + static_cast<size_t>(j) * kDPad;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 k4 = *reinterpret_cast<const f32x4 *>(kr + 16 * qq + 4 * i);
+                const f32x4 q4 = *reinterpret_cast<const f32x4 *>(q_s + 16 * qq + 4 * i);
+                acc = fmaf(q4[0], k4[0], acc);
+                acc = fmaf(q4[1], k4[1], acc);
+                acc = fmaf(q4[2], k4[2], acc);
+                acc = fmaf(q4[3], k4[3], acc);
+            }
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        if (kk < n) t = acc * a.scale_log2;
+    }
+    float m = t;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float p = kk < n ? fast_exp2(t - m) : 0.0f;
+    if (qq == 0) p_s[kk] = p;
+    // The sum of p over the chunk (each key counted by its qq == 0 thread).
+    float l = qq == 0 ? p : 0.0f;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+    __syncthreads();  // p_s complete; red[] read by everyone
+    if (lane == 0) red[w] = l;
+
+    // o = sum_j p_j v_j: lane = dim, wave w takes keys w, w + 4, ... (16 rows in flight).
+    float o = 0.0f;
+    {
+        float v[kDecChunk / 4];
+#pragma unroll
+        for (int u = 0; u < kDecChunk / 4; ++u) {
+            const int kj = w + 4 * u;
+            const int j = j0 + kj;
+            v[u] = kj < n ? ((j == pos) ? v_s[lane] : vc[static_cast<size_t>(j) * kDPad + lane]) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kDecChunk / 4; ++u) o = fmaf(p_s[w + 4 * u], v[u], o);
+    }
+    o_red[w][lane] = o;
+    __syncthreads();
+    if (tid < kDPad) {
+        float *rec = a.part + (static_cast<size_t>(bh) * a.splits + sp) * kDecPartStride;
+        rec[tid] = (o_red[0][tid] + o_red[1][tid]) + (o_red[2][tid] + o_red[3][tid]);
+        if (tid == 0) {
+            rec[kDPad] = m;
+            rec[kDPad + 1] = (red[0] + red[1]) + (red[2] + red[3]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void attn_decode_merge_kernel(const DecParams a) {
+    const int pos = a.pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*a.pos_dev) : a.pos;
+    if (pos < 0 || pos >= a.L) return;
+    const int bh = blockIdx.x, d = threadIdx.x;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int ns = pos / kDecChunk + 1;  // chunks holding keys
+    const float *rec = a.part + static_cast<size_t>(bh) * a.splits * kDecPartStride;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, rec[s * kDecPartStride + kDPad]);
+    float l = 0.0f, o = 0.0f;
+    for (int s = 0; s < ns; ++s) {
+        const float f = fast_exp2(rec[s * kDecPartStride + kDPad] - M);
+        l = fmaf(rec[s * kDecPartStride + kDPad + 1], f, l);
+        o = fmaf(rec[s * kDecPartStride + d], f, o);
+    }
+    a.out[static_cast<size_t>(b) * a.C + h * kDPad + d] = o / l;
+}
+
 void launch_attn_decode(const DecParams &p, hipStream_t stream) {
+    if (p.full && p.part != nullptr) {
+        attn_decode_split_kernel<<<dim3(p.B * p.H * p.splits), dim3(256), 0, stream>>>(p);
+        hipCheck(hipGetLastError());
+        attn_decode_merge_kernel<<<dim3(p.B * p.H), dim3(kDPad), 0, stream>>>(p);
+        hipCheck(hipGetLastError());
+        return;
+    }
     const size_t lds = static_cast<size_t>(p.pos_dev != nullptr ? p.L : p.pos + 1) * sizeof(float);
     attn_decode_kernel<<<dim3(p.B * p.H), dim3(kDecThreads), lds, stream>>>(p);
     hipCheck(hipGetLastError());

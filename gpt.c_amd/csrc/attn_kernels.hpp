@@ -77,9 +77,19 @@ struct DecParams {
                           // (graph replays); the score buffer is then sized for L keys
     float scale_log2;     // log2(e) / sqrt(D)
     bool full;            // D == kDPad and 16-byte aligned cache rows
+    float *part;          // if set (and full): split-key partials, B*H*splits*kDecPartStride floats
+    int splits;           // key chunks of kDecChunk per (b, h) (split path)
 };
 
 constexpr int kDecMaxKeys = 8192;  // pos + 1 limit (the scores live in LDS)
+constexpr int kDecChunk = 64;      // keys per workgroup of the split-key decode
+constexpr int kDecPartStride = 68; // floats per partial: o[64], m, l, 2 unused
+
+// Floats of the partials buffer of the split-key decode for B sequences of
+// H heads attending up to n_keys keys.
+inline size_t dec_part_floats(int B, int H, int n_keys) {
+    return static_cast<size_t>(B) * H * ((n_keys + kDecChunk - 1) / kDecChunk) * kDecPartStride;
+}
 
 void launch_attn_decode(const DecParams &p, hipStream_t stream);
 

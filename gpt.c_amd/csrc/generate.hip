@@ -23,7 +23,7 @@ using namespace gptc;
 
 namespace {
 
-enum { S_X, S_H, S_QKV, S_A, S_X2, S_MEAN, S_RSTD, S_F };
+enum { S_X, S_PART, S_QKV, S_A, S_X2, S_MEAN, S_RSTD, S_F };  // S_PART: split-key decode partials
 
 // The blocks, ln_f and lm_head of one step, from s[S_X] to logits.  pos_dev
 // set: the attention reads the position from device memory.
@@ -37,7 +37,7 @@ void step_body(gpt2_t *gpt, gptc_kv_cache_t *kv, int pos, const int *pos_dev, te
         const mlp_t *mlp = blk->mlp;
         ln_linear_rows(blk->ln1->W, blk->ln1->b, blk->ln1->eps, sa->qkv->W, sa->qkv->b, s[S_X], NULL, 0, s[S_QKV]);
         if (pos_dev != nullptr)
-            attention_decode_devpos(s[S_QKV], kv->k[l], kv->v[l], pos_dev, gpt->n_heads, s[S_A]);
+            attention_decode_devpos(s[S_QKV], kv->k[l], kv->v[l], pos_dev, gpt->n_heads, s[S_A], s[S_PART]->t);
         else
             attention_decode_cuda_kernel(s[S_QKV], kv->k[l], kv->v[l], pos, gpt->n_heads, s[S_A]);
         gptc_linear_rows_cuda(sa->c_proj->W, sa->c_proj->b, s[S_A], s[S_X], 0, s[S_X2]);
@@ -84,7 +84,8 @@ extern "C" gptc_kv_cache_t *gptc_kv_cache_create(const gpt2_t *gpt, const int B,
     int s_bc[3] = {B, 1, C}, s_b3c[3] = {B, 1, 3 * C}, s_b[1] = {B}, s_b4c[3] = {B, 1, 4 * C};
     int s_bv[3] = {B, 1, gpt->vocab_size};
     kv->scratch[S_X] = create_tensor(s_bc, 3, CUDA);
-    kv->scratch[S_H] = create_tensor(s_bc, 3, CUDA);
+    int s_part[1] = {static_cast<int>(attention_decode_part_floats(B, H, L))};
+    kv->scratch[S_PART] = create_tensor(s_part, 1, CUDA);
     kv->scratch[S_QKV] = create_tensor(s_b3c, 3, CUDA);
     kv->scratch[S_A] = create_tensor(s_bc, 3, CUDA);
     kv->scratch[S_X2] = create_tensor(s_bc, 3, CUDA);
