@@ -276,25 +276,31 @@ def c4_bench(args):
     model.to(gptc.CUDA)
     prompt = np.random.default_rng(SEED_X).integers(0, V, prompt_len)
     new = total - prompt_len
-    kv_generate(rt, model, prompt, prompt_len + 8, block)  # warm-up
-    rt.sync()
-    t0 = time.perf_counter()
-    toks, _ = kv_generate(rt, model, prompt, total, block)
-    rt.sync()
-    kv_s = time.perf_counter() - t0
-    cache = gptc.KVCache(rt, model, 1, total)
-    graph_generate(rt, model, prompt, total, cache)  # warm-up: captures the step graph
-    rt.sync()
-    t0 = time.perf_counter()
-    gtoks = graph_generate(rt, model, prompt, total, cache)
-    graph_s = time.perf_counter() - t0
-    cache.free()
-    window_generate(rt, model, prompt, prompt_len + 2, block)  # warm-up
-    rt.sync()
-    t0 = time.perf_counter()
-    wtoks, _ = window_generate(rt, model, prompt, total, block)
-    rt.sync()
-    win_s = time.perf_counter() - t0
+    loops = set(args.c4_loops.split(","))
+    toks = gtoks = wtoks = None
+    kv_s = graph_s = win_s = float("nan")
+    if "eager" in loops:
+        kv_generate(rt, model, prompt, prompt_len + 8, block)  # warm-up
+        rt.sync()
+        t0 = time.perf_counter()
+        toks, _ = kv_generate(rt, model, prompt, total, block)
+        rt.sync()
+        kv_s = time.perf_counter() - t0
+    if "graph" in loops:
+        cache = gptc.KVCache(rt, model, 1, total)
+        graph_generate(rt, model, prompt, total, cache)  # warm-up: captures the step graph
+        rt.sync()
+        t0 = time.perf_counter()
+        gtoks = graph_generate(rt, model, prompt, total, cache)
+        graph_s = time.perf_counter() - t0
+        cache.free()
+    if "window" in loops:
+        window_generate(rt, model, prompt, prompt_len + 2, block)  # warm-up
+        rt.sync()
+        t0 = time.perf_counter()
+        wtoks, _ = window_generate(rt, model, prompt, total, block)
+        rt.sync()
+        win_s = time.perf_counter() - t0
     model.free()
     g_tok = graph_s / (total - 1)
     # Per generated token the decode path reads every weight once (the tied
@@ -317,7 +323,9 @@ def c4_bench(args):
                              "tokens_per_s": round(new / win_s, 1),
                              "note": "infer_gpt.c's loop: the 1024-token window through GPT2.forward per token"},
         "speedup_graph_vs_window": round(win_s / graph_s, 1),
-        "same_tokens": bool(np.array_equal(toks, wtoks) and np.array_equal(gtoks, toks)),
+        "same_tokens": all(np.array_equal(u, v) for u, v in ((toks, wtoks), (gtoks, toks), (gtoks, wtoks))
+                           if u is not None and v is not None),
+        "loops": sorted(loops),
     }), flush=True)
     rt.sync()
 
@@ -462,6 +470,8 @@ def main():
                     help="copy: HBM copy of known size, to calibrate rocprof byte counters; "
                          "decode: the C4 KV-cache decode step; gpt2: the C3 GPT-2 124M training step; "
                          "c4: C4 greedy generation with GPT-2 124M")
+    ap.add_argument("--c4-loops", default="eager,graph,window",
+                    help="c4 workload: the loops to time (comma list of eager, graph, window)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
