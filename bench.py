@@ -597,8 +597,11 @@ def main():
     # HBM bytes per launch of the dominant kernel, from the committed rocprof
     # byte-counter runs (scaled by a plain copy; see profiles/).
     traffic_file = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.config}.json")
-    kernel_symbol = {"fwd": "attn_fwd_kernel", "bwd_delta": "attn_bwd_delta_kernel",
-                     "bwd_dkdv": "attn_bwd_dkdv_kernel", "bwd_dq": "attn_bwd_dq_kernel"}[dom]
+    # D = 64 runs the 16-row forward and dq kernels; other head sizes the 32-row ones.
+    kernel_symbols = {"fwd": ("attn_fwd16_kernel", "attn_fwd_kernel"), "bwd_delta": ("attn_bwd_delta_kernel",),
+                      "bwd_dkdv": ("attn_bwd_dkdv_kernel",),
+                      "bwd_dq": ("attn_bwd_dq16_kernel", "attn_bwd_dq_kernel")}[dom]
+    kernel_symbol = kernel_symbols[0] if D == 64 else kernel_symbols[-1]
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
             tr = json.load(f)["kernels"].get(kernel_symbol)

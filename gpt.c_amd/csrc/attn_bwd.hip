@@ -18,9 +18,12 @@
 //                          dP, dS, dV += P^T dO, dK += dS^T Q.  dS
 //                          overwrites P' in place, in the exact register
 //                          layout the dq kernel consumes it in.
-//   attn_bwd_dq_kernel     query-parallel: dQ^T += K^T dS^T.
+//   attn_bwd_dq16_kernel   query-parallel, D == 64: dQ += dS K, 16 queries
+//                          per wave, paired 64-query blocks per workgroup.
+//   attn_bwd_dq_kernel     query-parallel, other D: dQ^T += K^T dS^T.
 // The accumulator of the score product is directly the operand of the
 // gradient products (see the layout note in attn_common.hpp).
+#include <type_traits>
 #include "attn_common.hpp"
 #include "attn_kernels.hpp"
 #include "hip_check.hpp"
@@ -370,6 +373,136 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
         }
 }
 
+// ---- dQ, 16-row paired form (D == kDPad, 16-byte rows, 31-bit head sizes) ----
+// WG = 4 waves x 16 queries = one 64-query block j of one (b, h), then block
+// nqt-1-j of the same head, so every WG reduces nqt+1 key tiles and the grid
+// ((nqt+1)/2 x heads) is resident at once with equal work per WG.
+// v_mfma_f32_16x16x4_f32 on dQ[q][d] += sum_k dS[q][k] K[k][d]:
+//   A = dS (lane l: query l%16, k-slot l/16), B = K (k-slot l/16, column l%16).
+// Step (t, c) of a 64-key tile puts key 16t + 4j + c in k-slot j, so the A
+// operands of a lane for c = 0..3 are one float4 of its dS row and its B
+// operands one float4 of the K tile, which LDS holds as
+//     k_lds[(key / 4) * 256 + 4 * (16 * (d % 4) + d / 4) + key % 4]
+// (16 lanes read 256 contiguous bytes).  Column n of dim block db is dim
+// 4n + db: a lane ends with dims 4n .. 4n+3 of its rows, one float4 store each.
+// dS is read only where the wave's queries see the keys: on the block's own
+// tile, 16-key slices t <= w (the rest of that tile is zero).
+constexpr int kDq16KStride = 256;  // floats per group of 4 keys in k_lds
+
+__global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
+    __shared__ __attribute__((aligned(16))) float k_lds[16 * kDq16KStride];
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, j = lane >> 4, n = lane & 15;
+
+    // All pairs of a head on one XCD (blockIdx % 8): its K and dS blocks stay
+    // in that XCD's L2.
+    const int nbh_x = a.bh_pad / kXcds;
+    const int idx = blockIdx.x / kXcds;
+    const int pair = idx / nbh_x;
+    const int bh = blockIdx.x % kXcds + kXcds * (idx - pair * nbh_x);
+    if (bh >= a.B * a.H) return;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int T = a.T, nqt = a.nqt;
+    const int jA = pair, jB = nqt - 1 - pair;  // jB == jA: the middle block of an odd nqt, alone
+    const int nA = jA + 1;
+    const int n_steps = nA + (jB != jA ? jB + 1 : 0);
+
+    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+    const auto k_rows = head_rows(Kh, T, a.k.st);
+    // Cooperative K tile load: thread (kg, c4) reads keys 4kg .. 4kg+3, dims
+    // 4c4 .. 4c4+3 (rows past T read as zeros).
+    const int kg = tid >> 4, c4 = tid & 15;
+    f32x4 kpre[4];
+    auto prefetch_k = [&](int kt) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t key = kt * kBwdBQ + 4 * kg + c;
+            kpre[c] = buffer_load4(k_rows, key * a.k.st + 4 * c4);
+        }
+    };
+    // dS of the wave's 16 rows for tile kt of block jq: slice t (keys
+    // 16t .. 16t+15) lies in block 2kt + t/2, columns 16(t%2) ...
+    f32x4 dsn[4];
+    auto prefetch_ds = [&](int jq, int kt) {
+        if (jq * kBwdBQ + 16 * w >= T) return;  // rows wholly past T: nothing to reduce
+        const int nt = kt == jq ? w + 1 : 4;
+        const float *base = a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh, nqt, jq, 2 * kt)));
+        const uint32_t off = (16 * w + n) * 32 + 4 * j;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            if (t < nt) dsn[t] = *reinterpret_cast<const f32x4 *>(base + (t >> 1) * kDsBlock + off + 16 * (t & 1));
+    };
+    prefetch_k(0);
+    prefetch_ds(jA, 0);
+
+    f32x4 acc[4];  // acc[db][r] = dQ[q0 + 4j + r][4n + db] before the 1/sqrt(D) scaling
+    f32x4 dsc[4];
+    auto tile = [&](auto nt_c) {
+        constexpr int NT = decltype(nt_c)::value;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const f32x4 kb = *reinterpret_cast<const f32x4 *>(&k_lds[(4 * t + j) * kDq16KStride + 4 * (16 * db + n)]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[db] = mfma16(dsc[t][c], kb[c], acc[db]);
+            }
+    };
+
+    for (int s = 0; s < n_steps; ++s) {
+        const bool second = s >= nA;
+        const int jq = second ? jB : jA;     // query block
+        const int kt = second ? s - nA : s;  // key tile
+        const int q0 = jq * kBwdBQ + 16 * w;
+        if (kt == 0) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] = zero4();
+        }
+
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f32x4 v = {kpre[0][e], kpre[1][e], kpre[2][e], kpre[3][e]};
+            *reinterpret_cast<f32x4 *>(&k_lds[kg * kDq16KStride + 4 * (16 * e + c4)]) = v;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dsc[t] = dsn[t];
+        __syncthreads();
+        if (s + 1 < n_steps) {
+            const bool nsecond = s + 1 >= nA;
+            const int nkt = nsecond ? s + 1 - nA : s + 1;
+            prefetch_k(nkt);
+            prefetch_ds(nsecond ? jB : jA, nkt);
+        }
+
+        if (q0 >= T) continue;  // wave-uniform
+        const bool diag = kt == jq;
+        if (!diag) {
+            tile(IntC<4>{});
+            continue;
+        }
+        switch (w) {  // wave-uniform
+            case 0: tile(IntC<1>{}); break;
+            case 1: tile(IntC<2>{}); break;
+            case 2: tile(IntC<3>{}); break;
+            default: tile(IntC<4>{}); break;
+        }
+        // End of the block: dQ rows q0 + 4j + r.
+        float *dQh = a.dq.p + b * a.dq.sb + h * a.dq.sh + 4 * n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int q = q0 + 4 * j + r;
+            if (q < T) {
+                const f32x4 val = {acc[0][r] * a.scale, acc[1][r] * a.scale, acc[2][r] * a.scale,
+                                   acc[3][r] * a.scale};
+                *reinterpret_cast<f32x4 *>(dQh + q * a.dq.st) = val;
+            }
+        }
+    }
+}
+
 size_t bwd_ds_floats(int B, int H, int T) {
     const size_t nqt = (T + kBwdBQ - 1) / kBwdBQ;
     return static_cast<size_t>(B) * H * nqt * (nqt + 1) * kDsBlock;
@@ -377,9 +510,7 @@ size_t bwd_ds_floats(int B, int H, int T) {
 
 void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     BwdParams p = p_in;
-    if (p.full)
-        p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<true, true>);
-    else if (p.vec)
+    if (p.vec)
         p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<true, false>);
     else
         p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<false, false>);
@@ -408,7 +539,7 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
         hipCheck(hipEventRecord(ev[4], stream));
     }
     if (p.full)
-        attn_bwd_dq_kernel<true, true><<<grid_q, block, 0, stream>>>(p);
+        attn_bwd_dq16_kernel<<<dim3(((p.nqt + 1) / 2) * p.bh_pad), block, 0, stream>>>(p);
     else if (p.vec)
         attn_bwd_dq_kernel<true, false><<<grid_q, block, 0, stream>>>(p);
     else

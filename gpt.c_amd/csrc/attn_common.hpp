@@ -12,6 +12,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <cstdint>
 
 namespace gptc {
@@ -87,6 +88,10 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // A wave-uniform value the compiler cannot prove uniform (it would otherwise
 // keep it in VGPRs, and a buffer resource in VGPRs costs a waterfall loop
 // around every load).
+// A compile-time int argument (tile variants chosen by a uniform switch).
+template <int N>
+using IntC = std::integral_constant<int, N>;
+
 __device__ __forceinline__ uint32_t uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
 template <typename T>

@@ -256,9 +256,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // out in the same packed layout, so the backward is unchanged.
 constexpr int kF16Rows = 64;  // queries per block of the 16-row kernel (4 waves x 16)
 
-template <int N>
-using IntC = std::integral_constant<int, N>;
-
 template <bool PERM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_fwd16_kernel(const FwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
