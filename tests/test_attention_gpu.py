@@ -119,8 +119,8 @@ def test_c5_fwd_bwd_b4_t1024_h25(rt, oracle):
 
 
 def test_odd_block_count_wide_grid(rt, oracle):
-    """T = 960: 15 query blocks of 64, so one block of each head has no
-    partner, on a grid large enough for the three-sub-group workgroups."""
+    """T = 960: 15 query blocks of 64, so in the paired forward and dq grids
+    (blocks j and 14-j per workgroup) the middle block of each head runs alone."""
     compare_with_oracle(rt, oracle, 8, 960, 768, 12, sample_heads=[(0, 0), (5, 6), (7, 11)])
 
 
