@@ -7,7 +7,8 @@
 // added into dW in a fixed order, so it fills the GPU and stays deterministic.
 // The column sums are deterministic: workgroups sum fixed row ranges into a
 // partial buffer, and a second kernel adds the partials in a fixed order
-// (the reference uses one atomicAdd per workgroup and column).
+// (the reference uses one atomicAdd per workgroup and column); float4
+// columns where the shape allows.
 #include "blas.hpp"
 #include "gpu_kernels.h"
 #include "ops_common.hpp"
@@ -84,6 +85,77 @@ __global__ __launch_bounds__(kPartialWaves * kWave) void add_column_partials_ker
     }
 }
 
+// The same two reductions on float4 columns (cols % 4 == 0, 16-byte aligned
+// rows), with several loads in flight per lane.
+// partial[blockIdx.y, c] = sum of g[r, c] over rows r0 .. r0+rpp-1 of part
+// blockIdx.y: wave w takes rows r0 + w, r0 + w + 4, ... into two alternating
+// sums; the sums are added in a fixed order (sum 0 + sum 1 per wave, then
+// waves 0..3).
+__global__ __launch_bounds__(kThreads) void colsum_partial4_kernel(const float *__restrict__ g,
+                                                                  float *__restrict__ partial, int rows, int cols,
+                                                                  int rpp) {
+    __shared__ f32x4_t red[kThreads / kWave][kWave];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int n4 = cols / 4, c4 = blockIdx.x * kWave + lane;
+    const int r0 = blockIdx.y * rpp, r1 = min(rows, r0 + rpp);
+    const f32x4_t *g4 = reinterpret_cast<const f32x4_t *>(g);
+    f32x4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+    if (c4 < n4) {
+        int r = r0 + w;
+        for (; r + 4 < r1; r += 8) {
+            a0 += g4[static_cast<int64_t>(r) * n4 + c4];
+            a1 += g4[static_cast<int64_t>(r + 4) * n4 + c4];
+        }
+        if (r < r1) a0 += g4[static_cast<int64_t>(r) * n4 + c4];
+    }
+    red[w][lane] = a0 + a1;
+    __syncthreads();
+    if (w == 0 && c4 < n4) {
+        f32x4_t t = red[0][lane];
+#pragma unroll
+        for (int i = 1; i < kThreads / kWave; ++i) t += red[i][lane];
+        reinterpret_cast<f32x4_t *>(partial)[static_cast<int64_t>(blockIdx.y) * n4 + c4] = t;
+    }
+}
+
+constexpr int kSlices = 32;  // part slices per workgroup of add_column_partials4_kernel
+
+// out[c] += sum over p < parts of partial[p, c]: thread (slice sl, float4
+// column c4) adds parts sl, sl + 32, ... into four alternating sums (added in
+// order), and the 32 slice sums are then added in slice order.
+__global__ __launch_bounds__(kThreads) void add_column_partials4_kernel(const float *__restrict__ partial,
+                                                                       float *__restrict__ out, int parts, int cols) {
+    constexpr int kGroups = kThreads / kSlices;  // float4 columns per workgroup
+    __shared__ f32x4_t red[kSlices][kGroups];
+    const int cl = threadIdx.x % kGroups, sl = threadIdx.x / kGroups;
+    const int n4 = cols / 4, c4 = blockIdx.x * kGroups + cl;
+    const f32x4_t *p4 = reinterpret_cast<const f32x4_t *>(partial);
+    f32x4_t a[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (c4 < n4) {
+        int p = sl;
+        for (; p + 3 * kSlices < parts; p += 4 * kSlices)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) a[k] += p4[static_cast<int64_t>(p + k * kSlices) * n4 + c4];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)  // at most three parts are left
+            if (p + k * kSlices < parts) a[k] += p4[static_cast<int64_t>(p + k * kSlices) * n4 + c4];
+    }
+    red[sl][cl] = (a[0] + a[1]) + (a[2] + a[3]);
+    __syncthreads();
+    if (sl == 0 && c4 < n4) {
+        f32x4_t t = red[0][cl];
+#pragma unroll
+        for (int i = 1; i < kSlices; ++i) t += red[i][cl];
+        f32x4_t o = reinterpret_cast<f32x4_t *>(out)[c4];
+        o += t;
+        reinterpret_cast<f32x4_t *>(out)[c4] = o;
+    }
+}
+
+bool aligned16p(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
 
 void launch_bias_add(float *y, const float *b, int64_t rows, int cols, hipStream_t s) {
@@ -96,6 +168,20 @@ void launch_bias_add(float *y, const float *b, int64_t rows, int cols, hipStream
 // out[c] += sum_r g[r, c] for a row-major (rows x cols) g, deterministic.
 void launch_column_sum_add(const float *g, float *out, int rows, int cols, hipStream_t s) {
     if (rows <= 0 || cols <= 0) return;
+    if (cols % 4 == 0 && aligned16p(g) && aligned16p(out)) {
+        // About 1024 workgroups of 256 float4 columns x rpp rows.
+        const int cblocks = (cols / 4 + kWave - 1) / kWave;
+        int parts = (1024 + cblocks - 1) / cblocks;
+        if (parts > rows) parts = rows;
+        const int rpp = (rows + parts - 1) / parts;
+        parts = (rows + rpp - 1) / rpp;
+        float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * static_cast<size_t>(parts) * cols));
+        colsum_partial4_kernel<<<dim3(cblocks, parts), dim3(kThreads), 0, s>>>(g, partial, rows, cols, rpp);
+        hipCheck(hipGetLastError());
+        launch_add_column_partials(partial, out, parts, cols, s);
+        free_cuda(partial);
+        return;
+    }
     const int cblocks = (cols + kWave - 1) / kWave;
     int parts = 1024 / cblocks;
     const int max_parts = (rows + 3) / 4;
@@ -111,6 +197,13 @@ void launch_column_sum_add(const float *g, float *out, int rows, int cols, hipSt
 
 void launch_add_column_partials(const float *partial, float *out, int parts, int cols, hipStream_t s) {
     if (parts <= 0 || cols <= 0) return;
+    if (cols % 4 == 0 && aligned16p(partial) && aligned16p(out)) {
+        const int groups = kThreads / kSlices;
+        add_column_partials4_kernel<<<dim3((cols / 4 + groups - 1) / groups), dim3(kThreads), 0, s>>>(partial, out,
+                                                                                                     parts, cols);
+        hipCheck(hipGetLastError());
+        return;
+    }
     add_column_partials_kernel<<<dim3((cols + kWave - 1) / kWave), dim3(kPartialWaves * kWave), 0, s>>>(partial, out,
                                                                                                      parts, cols);
     hipCheck(hipGetLastError());
