@@ -5,7 +5,8 @@
 //             rows of -log_softmax[target];
 //   backward  with s = -g / (B T):  dout[j] = [j == target] s - exp(lsm[j]) s.
 // A row is one 256-thread workgroup: one online (max, sum) pass over the
-// logits, then a pass that writes the log-softmax.  The per-row losses go to
+// logits, then a pass that writes the log-softmax (float4 accesses and exp2
+// where the buffers are 16-byte aligned).  The per-row losses go to
 // a buffer and one workgroup adds them in a fixed order, so the mean is
 // deterministic.  A target outside [0, V) makes that row's loss NaN (the
 // reference would read outside the row) and its gradient row is the softmax
@@ -84,6 +85,116 @@ __global__ __launch_bounds__(kThreads) void ce_bwd_kernel(const float *__restric
     }
 }
 
+// The same two kernels on float4 vectors, for 16-byte aligned buffers.  Row r
+// starts at element r V; its first `head` elements (up to the next 16-byte
+// boundary) and its last V - head - 4 n4 are handled one per thread, the rest
+// as float4.  The exponentials are exp2 of log2(e)-scaled values
+// (v_exp_f32), and the running (max, sum) is kept in log2 units.
+constexpr float kLog2eF = 1.4426950408889634f;
+constexpr float kLn2F = 0.6931471805599453f;
+
+__device__ __forceinline__ void online_merge2(float &m, float &s, float m2, float s2) {
+    const float mn = fmaxf(m, m2);
+    if (mn == -INFINITY) return;  // both empty
+    s = s * __builtin_amdgcn_exp2f(m - mn) + s2 * __builtin_amdgcn_exp2f(m2 - mn);
+    m = mn;
+}
+
+__device__ __forceinline__ void row_split(int64_t base, int V, int &head, int &n4) {
+    head = static_cast<int>((4 - (base & 3)) & 3);
+    if (head > V) head = V;
+    n4 = (V - head) / 4;
+}
+
+// Index of the single element this thread handles at the row's unaligned
+// ends (threads 0..2: the head, 3..5: the tail), or -1.
+__device__ __forceinline__ int row_end_index(int head, int tail, int V) {
+    const int t = threadIdx.x;
+    if (t < head) return t;
+    if (t >= 3 && t < 6 && tail + (t - 3) < V) return tail + (t - 3);
+    return -1;
+}
+
+__global__ __launch_bounds__(kThreads) void ce_fwd4_kernel(const float *__restrict__ logits,
+                                                          const float *__restrict__ targets, float *__restrict__ lsm,
+                                                          float *__restrict__ row_loss, int V) {
+    __shared__ float sm[kWaves], ss[kWaves];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * V;
+    const float *xr = logits + base;
+    int head, n4;
+    row_split(base, V, head, n4);
+    const int je = row_end_index(head, head + 4 * n4, V);
+    const f32x4_t *x4 = reinterpret_cast<const f32x4_t *>(xr + head);
+    float m = -INFINITY, s = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += kThreads) {
+        const f32x4_t v = x4[i] * kLog2eF;
+        const float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if (mx > m) {
+            s *= __builtin_amdgcn_exp2f(m - mx);
+            m = mx;
+        }
+        if (m != -INFINITY)
+            s += (__builtin_amdgcn_exp2f(v[0] - m) + __builtin_amdgcn_exp2f(v[1] - m)) +
+                 (__builtin_amdgcn_exp2f(v[2] - m) + __builtin_amdgcn_exp2f(v[3] - m));
+    }
+    if (je >= 0) {
+        const float v = xr[je] * kLog2eF;
+        if (v > m) {
+            s = s * __builtin_amdgcn_exp2f(m - v) + 1.0f;
+            m = v;
+        } else if (v != -INFINITY) {
+            s += __builtin_amdgcn_exp2f(v - m);
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, kWave), s2 = __shfl_xor(s, off, kWave);
+        online_merge2(m, s, m2, s2);
+    }
+    const int w = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        sm[w] = m;
+        ss[w] = s;
+    }
+    __syncthreads();
+    m = sm[0];
+    s = ss[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) online_merge2(m, s, sm[i], ss[i]);
+    const float shift = (m + log2f(s)) * kLn2F;  // log of the row's sum of exp
+    float *lr = lsm + base;
+    f32x4_t *l4 = reinterpret_cast<f32x4_t *>(lr + head);
+    for (int i = threadIdx.x; i < n4; i += kThreads) l4[i] = x4[i] - shift;
+    if (je >= 0) lr[je] = xr[je] - shift;
+    if (threadIdx.x == 0) {
+        const int t = static_cast<int>(targets[blockIdx.x]);
+        row_loss[blockIdx.x] = (t >= 0 && t < V) ? -(xr[t] - shift) : NAN;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void ce_bwd4_kernel(const float *__restrict__ g, const float *__restrict__ lsm,
+                                                          const float *__restrict__ targets, float *__restrict__ dout,
+                                                          int V, float rows_f) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * V;
+    const float s = -g[blockIdx.x] / rows_f;
+    const int t = static_cast<int>(targets[blockIdx.x]);
+    int head, n4;
+    row_split(base, V, head, n4);
+    const int je = row_end_index(head, head + 4 * n4, V);
+    const float *lr = lsm + base;
+    float *dr = dout + base;
+    const f32x4_t *l4 = reinterpret_cast<const f32x4_t *>(lr + head);
+    f32x4_t *d4 = reinterpret_cast<f32x4_t *>(dr + head);
+    for (int i = threadIdx.x; i < n4; i += kThreads) {
+        const f32x4_t l = l4[i] * kLog2eF;
+        f32x4_t d;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) d[c] = (head + 4 * i + c == t ? s : 0.0f) - __builtin_amdgcn_exp2f(l[c]) * s;
+        d4[i] = d;
+    }
+    if (je >= 0) dr[je] = (je == t ? s : 0.0f) - __builtin_amdgcn_exp2f(lr[je] * kLog2eF) * s;
+}
+
 }  // namespace
 
 }  // namespace gptc
@@ -105,7 +216,10 @@ extern "C" void cross_entropy_forward_cuda_kernel(const tensor_t *logits, const 
     CHECK_ERROR(rows < 1 || V < 1, "Expected at least one row of logits.");
     hipStream_t s = gptc_stream_checked();
     float *row_loss = static_cast<float *>(alloc_cuda(sizeof(float) * rows));
-    ce_fwd_kernel<<<dim3(rows), dim3(kThreads), 0, s>>>(logits->t, targets->t, cache[0]->t, row_loss, V);
+    if (aligned16(logits->t) && aligned16(cache[0]->t))
+        ce_fwd4_kernel<<<dim3(rows), dim3(kThreads), 0, s>>>(logits->t, targets->t, cache[0]->t, row_loss, V);
+    else
+        ce_fwd_kernel<<<dim3(rows), dim3(kThreads), 0, s>>>(logits->t, targets->t, cache[0]->t, row_loss, V);
     hipCheck(hipGetLastError());
     ce_mean_kernel<<<dim3(1), dim3(kThreads), 0, s>>>(row_loss, output->t, rows);
     hipCheck(hipGetLastError());
@@ -126,7 +240,11 @@ extern "C" void cross_entropy_backward_cuda_kernel(const tensor_t *global_grad, 
     CHECK_ERROR(dout->length != lsm->length, "Expected dout to match the logits' %d elements.", lsm->length);
     if (rows == 0) return;
     // The reference divides by the int B*T (cpu/CrossEntropyLoss.c:67-72).
-    ce_bwd_kernel<<<dim3(rows), dim3(kThreads), 0, gptc_stream_checked()>>>(
-        global_grad->t, lsm->t, cache[1]->t, dout->t, V, static_cast<float>(rows));
+    if (aligned16(lsm->t) && aligned16(dout->t))
+        ce_bwd4_kernel<<<dim3(rows), dim3(kThreads), 0, gptc_stream_checked()>>>(
+            global_grad->t, lsm->t, cache[1]->t, dout->t, V, static_cast<float>(rows));
+    else
+        ce_bwd_kernel<<<dim3(rows), dim3(kThreads), 0, gptc_stream_checked()>>>(
+            global_grad->t, lsm->t, cache[1]->t, dout->t, V, static_cast<float>(rows));
     hipCheck(hipGetLastError());
 }
