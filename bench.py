@@ -102,8 +102,11 @@ def contraction_flops(B, T, H, D):
     return float(D) * T * (T + 1) * B * H
 
 
-def cpu_baseline(cfg, x, dy, budget_s):
-    """The oracle (C restatement of gpt.c's OpenBLAS CPU path) on this host."""
+def cpu_baseline(cfg, x, dy, budget_s, gpu_out=None):
+    """The oracle (C restatement of gpt.c's OpenBLAS CPU path) on this host.
+
+    gpu_out = (y, dqkv) of the timed GPU steps on the same inputs: the last
+    oracle run checks them (max abs error), as the parity tests do."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as oracle_mod
     threads = min(16, os.cpu_count() or 1)
@@ -113,9 +116,9 @@ def cpu_baseline(cfg, x, dy, budget_s):
     t_start = time.perf_counter()
     for i in range(4):
         t0 = time.perf_counter()
-        _, q, k, v, att = orc.forward(x, H)
+        y_ref, q, k, v, att = orc.forward(x, H)
         t1 = time.perf_counter()
-        orc.backward(dy, H, q, k, v, att)
+        d_ref = orc.backward(dy, H, q, k, v, att)
         t2 = time.perf_counter()
         if i > 0:
             times.append((t1 - t0, t2 - t1))
@@ -132,6 +135,10 @@ def cpu_baseline(cfg, x, dy, budget_s):
             model = m.group(1).strip() if m else ""
     except OSError:
         pass
+    err = None
+    if gpu_out is not None:
+        err = {"y": float(np.abs(gpu_out[0].astype(np.float64) - y_ref).max()),
+               "dqkv": float(np.abs(gpu_out[1].astype(np.float64) - d_ref).max())}
     return {
         "value": flops / (fwd + bwd) / 1e12,
         "unit": "TFLOP/s",
@@ -141,6 +148,7 @@ def cpu_baseline(cfg, x, dy, budget_s):
                    f"{len(times)}; fwd {fwd * 1e3:.1f} ms + bwd {bwd * 1e3:.1f} ms; OPENBLAS threads={threads}; "
                    f"{orc.blas_config}; host '{model}', nproc={os.cpu_count()}"),
         "ms_per_step": (fwd + bwd) * 1e3,
+        "gpu_max_abs_err": err,
     }
 
 
@@ -579,6 +587,11 @@ def main():
         "config": {"workload": cfg["workload"], "B": B, "T": T, "H": H, "D": D, "C": C,
                    "causal_flop_per_step": flops},
         "pct_fp32_mfma_peak": round(100.0 * value / peak, 2),
+        # FlashAttention's convention (full T^2 work, backward 2.5x forward), for comparison only.
+        "tflops_fa_convention": round(7.0 * B * H * T * T * D / (ms_per_step * 1e-3) / 1e12, 3),
+        # Compulsory HBM bytes: forward reads qkv, writes y and LSE; backward reads qkv, y, dy and LSE, writes dqkv.
+        "compulsory_gb_per_s": round(4.0 * (B * T * (3 * C + C) + B * H * T + B * T * (3 * C + 2 * C) + B * H * T +
+                                            B * T * 3 * C) / (ms_per_step * 1e-3) / 1e9, 1),
         "tokens_per_s": round(B * T / (ms_per_step * 1e-3), 1),
         "peak_tflops": round(peak, 2),
         "peak_source": f"{peak_src}: {cu} CU x {mhz} MHz x {FLOP_PER_CLK_CU_FP32_MFMA} flop/clk/CU",
@@ -608,13 +621,14 @@ def main():
         if tr:
             result["roofline"]["traffic"] = tr["read_bytes"] + tr["write_bytes"]
             result["roofline"]["traffic_source"] = f"profiles/hbm_traffic_{args.config}.json (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE)"
+    gpu_out = None if args.no_cpu_baseline else (rt.to_numpy(yt), rt.to_numpy(dqkv))
     for t in (dyt, mask, yt, dqkv, *caches):
         rt.free(t)
     rt.sync()
 
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle over OpenBLAS) ...")
-        cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s)
+        cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s, gpu_out)
         result["cpu_baseline"] = {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cb.items()}
     else:
         result["cpu_baseline"] = None
