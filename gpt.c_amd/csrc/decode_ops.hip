@@ -35,16 +35,18 @@ struct RowsArgs {
     int rows, in_f, out_f, act;
 };
 
-// The 4 waves of a workgroup own `kOuts` output features; for each, the
-// kSplit = 4 / kOuts waves on it take equal slices of the in_f inputs (so a
-// narrow output still puts work on every CU), and the slices' sums meet in
-// LDS.  acc[r] = W[o, :] . xn[r, :] for r < rows, where xn = x, or with kLN
-// the LayerNorm of each x row (mean and rstd computed by the workgroup: the
-// decode step's rows are at most 8 of a few thousand features).
-template <bool kVec, bool kLN, int kOuts>
+// The 4 waves of a workgroup own `kOuts` groups of kPer output features;
+// for each group, the kSplit = 4 / kOuts waves on it take equal slices of the
+// in_f inputs (so a narrow output still puts work on every CU), and the
+// slices' sums meet in LDS.  acc[p][r] = W[o_p, :] . xn[r, :] for r < rows,
+// where xn = x, or with kLN the LayerNorm of each x row (mean and rstd
+// computed by the workgroup: the decode step's rows are at most 8 of a few
+// thousand features).  kPer > 1 (wide outputs): a wave reads its normalised
+// x vector once for kPer weight rows, with kPer loads in flight.
+template <bool kVec, bool kLN, int kOuts, int kPer>
 __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a) {
     constexpr int kSplit = kWaves / kOuts;
-    __shared__ float part[kWaves][kMaxRows];
+    __shared__ float part[kWaves * kPer][kMaxRows];
     __shared__ float stat[2][kMaxRows];
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     const int in_f = a.in_f, rows = a.rows;
@@ -89,18 +91,24 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
         }
         __syncthreads();
     }
-    const int o = blockIdx.x * kOuts + w / kSplit;
-    const int slice = w % kSplit;
+    const int grp = w / kSplit, slice = w % kSplit;
+    const int o0 = (blockIdx.x * kOuts + grp) * kPer;  // this wave's first output
     const int per = (in_f + kSplit - 1) / kSplit;
     const int j0 = slice * per, j1 = min(in_f, j0 + per);
-    float acc[kMaxRows];
+    float acc[kPer][kMaxRows];
 #pragma unroll
-    for (int r = 0; r < kMaxRows; ++r) acc[r] = 0.0f;
-    if (o < a.out_f) {
-        const float *wrow = a.W + static_cast<int64_t>(o) * in_f;
+    for (int p = 0; p < kPer; ++p)
+#pragma unroll
+        for (int r = 0; r < kMaxRows; ++r) acc[p][r] = 0.0f;
+    if (o0 < a.out_f) {
         if (kVec) {  // in_f % (4 kSplit) == 0: slices are whole 16-byte vectors
             for (int j = j0 / 4 + lane; j < j1 / 4; j += kWave) {
-                const f32x4_t wv = reinterpret_cast<const f32x4_t *>(wrow)[j];
+                f32x4_t wv[kPer];
+#pragma unroll
+                for (int p = 0; p < kPer; ++p)
+                    wv[p] = o0 + p < a.out_f
+                                ? reinterpret_cast<const f32x4_t *>(a.W + static_cast<int64_t>(o0 + p) * in_f)[j]
+                                : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 f32x4_t lw = {1.0f, 1.0f, 1.0f, 1.0f}, lb = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (kLN) {
                     lw = reinterpret_cast<const f32x4_t *>(a.ln_w)[j];
@@ -114,40 +122,46 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
 #pragma unroll
                             for (int e = 0; e < 4; ++e) xv[e] = (xv[e] - stat[0][r]) * stat[1][r] * lw[e] + lb[e];
                         }
-                        acc[r] = fmaf(wv[0], xv[0], acc[r]);
-                        acc[r] = fmaf(wv[1], xv[1], acc[r]);
-                        acc[r] = fmaf(wv[2], xv[2], acc[r]);
-                        acc[r] = fmaf(wv[3], xv[3], acc[r]);
+#pragma unroll
+                        for (int p = 0; p < kPer; ++p) {
+                            acc[p][r] = fmaf(wv[p][0], xv[0], acc[p][r]);
+                            acc[p][r] = fmaf(wv[p][1], xv[1], acc[p][r]);
+                            acc[p][r] = fmaf(wv[p][2], xv[2], acc[p][r]);
+                            acc[p][r] = fmaf(wv[p][3], xv[3], acc[p][r]);
+                        }
                     }
                 }
             }
         } else {
             for (int j = j0 + lane; j < j1; j += kWave) {
-                const float wv = wrow[j];
 #pragma unroll
                 for (int r = 0; r < kMaxRows; ++r) {
                     if (r < rows) {
                         float xv = a.x[static_cast<int64_t>(r) * in_f + j];
                         if (kLN)
                             xv = (xv - stat[0][r]) * stat[1][r] * a.ln_w[j] + (a.ln_b != nullptr ? a.ln_b[j] : 0.0f);
-                        acc[r] = fmaf(wv, xv, acc[r]);
+#pragma unroll
+                        for (int p = 0; p < kPer; ++p)
+                            if (o0 + p < a.out_f)
+                                acc[p][r] = fmaf(a.W[static_cast<int64_t>(o0 + p) * in_f + j], xv, acc[p][r]);
                     }
                 }
             }
         }
     }
 #pragma unroll
-    for (int r = 0; r < kMaxRows; ++r)
-        if (r < rows) {
-            const float v = wave_sum(acc[r]);
-            if (lane == 0) part[w][r] = v;
-        }
+    for (int p = 0; p < kPer; ++p)
+#pragma unroll
+        for (int r = 0; r < kMaxRows; ++r)
+            if (r < rows) {
+                const float v = wave_sum(acc[p][r]);
+                if (lane == 0) part[(grp * kPer + p) * kSplit + slice][r] = v;
+            }
     __syncthreads();
     // One thread per (output, row) adds the slices in order and finishes.
-    const int t = threadIdx.x;
-    if (t < kOuts * rows) {
+    for (int t = threadIdx.x; t < kOuts * kPer * rows; t += kThreads) {
         const int oo = t / rows, r = t % rows;
-        const int out = blockIdx.x * kOuts + oo;
+        const int out = blockIdx.x * kOuts * kPer + oo;
         if (out < a.out_f) {
             float v = part[oo * kSplit][r];
 #pragma unroll
@@ -160,29 +174,29 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
     }
 }
 
-template <bool kLN, int kOuts>
+template <bool kLN, int kOuts, int kPer>
 void launch_rows(const RowsArgs &a, bool vec, hipStream_t s) {
-    const dim3 grid((a.out_f + kOuts - 1) / kOuts);
+    const dim3 grid((a.out_f + kOuts * kPer - 1) / (kOuts * kPer));
     if (vec)
-        linear_rows_kernel<true, kLN, kOuts><<<grid, dim3(kThreads), 0, s>>>(a);
+        linear_rows_kernel<true, kLN, kOuts, kPer><<<grid, dim3(kThreads), 0, s>>>(a);
     else
-        linear_rows_kernel<false, kLN, kOuts><<<grid, dim3(kThreads), 0, s>>>(a);
+        linear_rows_kernel<false, kLN, kOuts, kPer><<<grid, dim3(kThreads), 0, s>>>(a);
     hipCheck(hipGetLastError());
 }
 
 // Narrow outputs (under 4096 features) split each dot product over the 4
-// waves of a workgroup; wide ones give each wave its own feature.
+// waves of a workgroup; wide ones give each wave 4 features of its own.
 void run_rows(const RowsArgs &a, hipStream_t s) {
     const bool narrow = a.out_f < 4096;
     const int split = narrow ? 4 : 1;
     const bool vec = (a.in_f % (4 * split)) == 0 && aligned16(a.W) && aligned16(a.x) &&
                      (a.ln_w == nullptr || (aligned16(a.ln_w) && aligned16(a.ln_b)));
     if (a.ln_w != nullptr) {
-        if (narrow) launch_rows<true, 1>(a, vec, s);
-        else launch_rows<true, 4>(a, vec, s);
+        if (narrow) launch_rows<true, 1, 1>(a, vec, s);
+        else launch_rows<true, 4, 4>(a, vec, s);
     } else {
-        if (narrow) launch_rows<false, 1>(a, vec, s);
-        else launch_rows<false, 4>(a, vec, s);
+        if (narrow) launch_rows<false, 1, 1>(a, vec, s);
+        else launch_rows<false, 4, 4>(a, vec, s);
     }
 }
 
