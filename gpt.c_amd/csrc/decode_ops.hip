@@ -184,18 +184,21 @@ void launch_rows(const RowsArgs &a, bool vec, hipStream_t s) {
     hipCheck(hipGetLastError());
 }
 
-// Narrow outputs (under 4096 features) split each dot product over the 4
-// waves of a workgroup; wide ones give each wave 4 features of its own.
+// Narrow outputs (under 1024 features) split each dot product over the 4
+// waves of a workgroup; medium ones (under 4096) give each wave a feature of
+// its own, wide ones 4 features.
 void run_rows(const RowsArgs &a, hipStream_t s) {
-    const bool narrow = a.out_f < 4096;
-    const int split = narrow ? 4 : 1;
+    const int kind = a.out_f < 1024 ? 0 : a.out_f < 4096 ? 1 : 2;
+    const int split = kind == 0 ? 4 : 1;
     const bool vec = (a.in_f % (4 * split)) == 0 && aligned16(a.W) && aligned16(a.x) &&
                      (a.ln_w == nullptr || (aligned16(a.ln_w) && aligned16(a.ln_b)));
     if (a.ln_w != nullptr) {
-        if (narrow) launch_rows<true, 1, 1>(a, vec, s);
+        if (kind == 0) launch_rows<true, 1, 1>(a, vec, s);
+        else if (kind == 1) launch_rows<true, 4, 1>(a, vec, s);
         else launch_rows<true, 4, 4>(a, vec, s);
     } else {
-        if (narrow) launch_rows<false, 1, 1>(a, vec, s);
+        if (kind == 0) launch_rows<false, 1, 1>(a, vec, s);
+        else if (kind == 1) launch_rows<false, 4, 1>(a, vec, s);
         else launch_rows<false, 4, 4>(a, vec, s);
     }
 }
