@@ -159,7 +159,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
 // of kDecChunk, one 256-thread workgroup each, which writes the chunk's
 // partial softmax state (max m_s and sum l_s of exp2(t - m_s), unnormalised
 // o_s = sum p v); a second kernel merges the chunks of each (b, h):
-//   M = max m_s,  l = sum l_s exp2(m_s - M),  o = sum o_s exp2(m_s - M) / l.
+//   M = max m_s,  l = sum l_s exp2(m_s - M),  o = sum o_s exp2(m_s - M) / l
+// (computed in one pass as a running merge).
 // The workgroup holding key pos takes the new k, v from the qkv row and
 // writes them into the caches at pos; the others read cache rows below pos.
 __global__ __launch_bounds__(256) void attn_decode_split_kernel(const DecParams a) {
@@ -265,13 +266,18 @@ __global__ __launch_bounds__(64) void attn_decode_merge_kernel(const DecParams a
     const int b = bh / a.H, h = bh - b * a.H;
     const int ns = pos / kDecChunk + 1;  // chunks holding keys
     const float *rec = a.part + static_cast<size_t>(bh) * a.splits * kDecPartStride;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, rec[s * kDecPartStride + kDPad]);
-    float l = 0.0f, o = 0.0f;
+    // One pass, merging the chunks' states in order (their loads do not wait
+    // on each other; every chunk holds a key, so its m_s is finite).
+    float M = -INFINITY, l = 0.0f, o = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < ns; ++s) {
-        const float f = fast_exp2(rec[s * kDecPartStride + kDPad] - M);
-        l = fmaf(rec[s * kDecPartStride + kDPad + 1], f, l);
-        o = fmaf(rec[s * kDecPartStride + d], f, o);
+        const float ms = rec[s * kDecPartStride + kDPad], ls = rec[s * kDecPartStride + kDPad + 1];
+        const float os = rec[s * kDecPartStride + d];
+        const float mn = fmaxf(M, ms);
+        const float fa = fast_exp2(M - mn), fb = fast_exp2(ms - mn);
+        l = fmaf(l, fa, ls * fb);
+        o = fmaf(o, fa, os * fb);
+        M = mn;
     }
     a.out[static_cast<size_t>(b) * a.C + h * kDPad + d] = o / l;
 }
