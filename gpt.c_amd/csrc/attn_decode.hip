@@ -185,6 +185,15 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(const DecParams 
     const float *row = a.qkv + static_cast<size_t>(b) * 3 * a.C + h * kDPad;
     float *kc = a.k_cache + static_cast<size_t>(bh) * a.L * kDPad;
     float *vc = a.v_cache + static_cast<size_t>(bh) * a.L * kDPad;
+    // V rows of this lane (dim `lane`; wave w takes keys w, w + 4, ...), issued
+    // first so that their latency overlaps the score phase.  Key pos is
+    // replaced by the new v below.
+    float v[kDecChunk / 4];
+#pragma unroll
+    for (int u = 0; u < kDecChunk / 4; ++u) {
+        const int kj = w + 4 * u;
+        v[u] = kj < n ? vc[static_cast<size_t>(j0 + kj) * kDPad + lane] : 0.0f;
+    }
     if (tid < kDPad) {
         q_s[tid] = row[tid];
         if (has_pos) {
@@ -236,16 +245,11 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(const DecParams 
 
     // o = sum_j p_j v_j: lane = dim, wave w takes keys w, w + 4, ... (16 rows in flight).
     float o = 0.0f;
-    {
-        float v[kDecChunk / 4];
 #pragma unroll
-        for (int u = 0; u < kDecChunk / 4; ++u) {
-            const int kj = w + 4 * u;
-            const int j = j0 + kj;
-            v[u] = kj < n ? ((j == pos) ? v_s[lane] : vc[static_cast<size_t>(j) * kDPad + lane]) : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kDecChunk / 4; ++u) o = fmaf(p_s[w + 4 * u], v[u], o);
+    for (int u = 0; u < kDecChunk / 4; ++u) {
+        const int kj = w + 4 * u;
+        if (j0 + kj == pos) v[u] = v_s[lane];
+        o = fmaf(p_s[w + 4 * u], v[u], o);
     }
     o_red[w][lane] = o;
     __syncthreads();
