@@ -485,8 +485,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (every (b, h) pair of causal attention is "
-              "independent; see DESIGN.md for how the path shards). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU only. Every (b, h) pair of causal attention is independent, "
+              "so the path shards over batch or heads with no exchange. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.workload == "decode":
         decode_bench(args)
