@@ -31,11 +31,11 @@ import numpy as np  # noqa: E402
 
 import gptc  # noqa: E402
 
-METRIC = "causal attn fwd+bwd TFLOP/s + % fp32 MFMA peak, B=8 T=1024 H=12 D=64"
 CONFIGS = {
     "c2": dict(B=8, T=1024, C=768, H=12, workload="causal self-attention fwd+bwd, GPT-2 124M shape (C2)"),
     "c5": dict(B=4, T=1024, C=1600, H=25, workload="causal self-attention fwd+bwd, GPT-2 XL shape (C5)"),
-    "c1": dict(B=8, T=128, C=768, H=12, workload="causal self-attention fwd+bwd at C1's shape"),
+    "c1": dict(B=8, T=128, C=768, H=12, forward_only=True,
+               workload="causal self-attention forward only (C1), HBM-side of the ridge"),
 }
 SEED_X, SEED_DY = 1337, 1338
 SPEC_CU, SPEC_MHZ = 256, 2400            # MI355X public spec
@@ -103,22 +103,26 @@ def contraction_flops(B, T, H, D):
 
 
 def cpu_baseline(cfg, x, dy, budget_s, gpu_out=None):
-    """The oracle (C restatement of gpt.c's OpenBLAS CPU path) on this host.
+    """The oracle (C restatement of gpt.c's OpenBLAS CPU path) on this host,
+    forward + backward (forward only for a forward-only config).
 
-    gpu_out = (y, dqkv) of the timed GPU steps on the same inputs: the last
-    oracle run checks them (max abs error), as the parity tests do."""
+    gpu_out = {"y", "lse", "dqkv"} of the timed GPU steps on the same inputs:
+    the last oracle run checks them (max abs error per output; the LSE
+    against a float64 log-sum-exp of the oracle's q, k), as the parity tests
+    do."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as oracle_mod
     threads = min(16, os.cpu_count() or 1)
     orc = oracle_mod.Oracle(threads=threads)
     B, T, C, H = cfg["B"], cfg["T"], cfg["C"], cfg["H"]
+    fwd_only = bool(cfg.get("forward_only"))
     times = []
     t_start = time.perf_counter()
     for i in range(4):
         t0 = time.perf_counter()
         y_ref, q, k, v, att = orc.forward(x, H)
         t1 = time.perf_counter()
-        d_ref = orc.backward(dy, H, q, k, v, att)
+        d_ref = None if fwd_only else orc.backward(dy, H, q, k, v, att)
         t2 = time.perf_counter()
         if i > 0:
             times.append((t1 - t0, t2 - t1))
@@ -127,7 +131,6 @@ def cpu_baseline(cfg, x, dy, budget_s, gpu_out=None):
             break
     fwd = statistics.median(t[0] for t in times)
     bwd = statistics.median(t[1] for t in times)
-    flops = 6 * contraction_flops(B, T, H, C // H)
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -137,19 +140,24 @@ def cpu_baseline(cfg, x, dy, budget_s, gpu_out=None):
         pass
     err = None
     if gpu_out is not None:
-        err = {"y": float(np.abs(gpu_out[0].astype(np.float64) - y_ref).max()),
-               "dqkv": float(np.abs(gpu_out[1].astype(np.float64) - d_ref).max())}
-    return {
-        "value": flops / (fwd + bwd) / 1e12,
-        "unit": "TFLOP/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"one full {cfg['workload']} step (B={B} T={T} H={H}), 1 warm-up then median of "
-                   f"{len(times)}; fwd {fwd * 1e3:.1f} ms + bwd {bwd * 1e3:.1f} ms; OPENBLAS threads={threads}; "
-                   f"{orc.blas_config}; host '{model}', nproc={os.cpu_count()}"),
-        "ms_per_step": (fwd + bwd) * 1e3,
-        "gpu_max_abs_err": err,
-    }
+        def e(a, b):
+            return float(np.abs(a.astype(np.float64) - b).max())
+        err = {"y": e(gpu_out["y"], y_ref), "lse": e(gpu_out["lse"], lse_fp64(q, k))}
+        if not fwd_only:
+            d = gpu_out["dqkv"]
+            err.update(dq=e(d[..., :C], d_ref[..., :C]), dk=e(d[..., C:2 * C], d_ref[..., C:2 * C]),
+                       dv=e(d[..., 2 * C:], d_ref[..., 2 * C:]))
+        err["tolerance"] = 1e-4
+    sample = (f"one full {cfg['workload']} call (B={B} T={T} H={H}), 1 warm-up then median of {len(times)}; "
+              f"fwd {fwd * 1e3:.1f} ms" + ("" if fwd_only else f" + bwd {bwd * 1e3:.1f} ms") +
+              f"; OPENBLAS threads={threads}; {orc.blas_config}; host '{model}', nproc={os.cpu_count()}")
+    if fwd_only:
+        fwd_bytes, _ = compulsory_bytes(B, T, C, H)
+        value, unit, ms = fwd_bytes / fwd / 1e9, "GB/s", fwd * 1e3
+    else:
+        value, unit, ms = 6 * contraction_flops(B, T, H, C // H) / (fwd + bwd) / 1e12, "TFLOP/s", (fwd + bwd) * 1e3
+    return {"value": value, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
+            "ms_per_step": ms, "gpu_max_abs_err": err}
 
 
 def copy_calibration(args):
@@ -263,22 +271,13 @@ def c4_bench(args):
     for every token).  Both produce the same tokens (tests/test_generate_gpu.py);
     here they are timed end to end, host loop included."""
     from generation import graph_generate, kv_generate, window_generate
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from gpt2_oracle import param_shapes
     V, block, L, H, C, prompt_len, total = 50257, 1024, 12, 12, 768, 64, 512
     lib = gptc.load()
     rt = gptc.Runtime(lib)
     rt.init()
-    params = []
-    for i, (name, shp) in enumerate(param_shapes(V, block, L, C)):
-        if name.endswith(("ln1.W", "ln2.W")) or name == "ln_f.W":
-            params.append(np.ones(shp, np.float32))
-        elif len(shp) == 1:
-            params.append(np.zeros(shp, np.float32))
-        else:
-            params.append(rt.normal(shp, 1000 + i, 0.0, 0.02))
-    n_weights = sum(p.size for p in params)
     model = gptc.GPT2Model(rt, block, V, L, H, C)
+    params = model.random_init_arrays()
+    n_weights = sum(p.size for p in params)
     model.fast_load(params)
     del params
     model.to(gptc.CUDA)
@@ -388,22 +387,12 @@ def gpt2_bench(args):
     rt.init()
     hip = Hip()
     stream = rt.stream()
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from gpt2_oracle import param_shapes  # names and shapes only
-
-    params = []
-    for i, (name, shp) in enumerate(param_shapes(V, block, L, C)):
-        if name.endswith(("ln1.W", "ln2.W")) or name == "ln_f.W":
-            params.append(np.ones(shp, np.float32))
-        elif len(shp) == 1:
-            params.append(np.zeros(shp, np.float32))
-        else:
-            params.append(rt.normal(shp, 1000 + i, 0.0, 0.02))
     rng = np.random.default_rng(SEED_X)
     ids = rt.from_numpy(rng.integers(0, V, (B, T)).astype(np.float32))
     tgs = rt.from_numpy(rng.integers(0, V, (B, T)).astype(np.float32))
     ones = rt.from_numpy(np.ones((B, T), np.float32))
     model = gptc.GPT2Model(rt, block, V, L, H, C)
+    params = model.random_init_arrays()
     model.fast_load(params)
     del params
     model.to(gptc.CUDA)
@@ -468,6 +457,265 @@ def gpt2_bench(args):
     rt.sync()
 
 
+def attention_metric(cfg):
+    """The metric string of a config: BASELINE.json's for C2, the same form
+    with each config's own shape otherwise; C1 is forward-only and HBM-side,
+    so its metric is compulsory GB/s."""
+    B, T, H, D = cfg["B"], cfg["T"], cfg["H"], cfg["C"] // cfg["H"]
+    if cfg.get("forward_only"):
+        return f"causal attn fwd compulsory HBM GB/s (cold MALL), B={B} T={T} H={H} D={D}"
+    return f"causal attn fwd+bwd TFLOP/s + % fp32 MFMA peak, B={B} T={T} H={H} D={D}"
+
+
+def compulsory_bytes(B, T, C, H):
+    """Compulsory HBM bytes: forward reads qkv, writes y and the LSE;
+    backward reads qkv, y, dy and the LSE, writes dqkv."""
+    fwd = 4.0 * (B * T * (3 * C + C) + B * H * T)
+    bwd = 4.0 * (B * T * (3 * C + 2 * C) + B * H * T + B * T * 3 * C)
+    return fwd, bwd
+
+
+def lse_fp64(q, k):
+    """Natural-log causal row log-sum-exp of (B, H, T, D) q, k in float64."""
+    B, H, T, D = q.shape
+    out = np.empty((B, H, T))
+    keep = np.tril(np.ones((T, T), bool))
+    for b in range(B):
+        s = np.matmul(q[b].astype(np.float64), k[b].astype(np.float64).transpose(0, 2, 1)) / np.sqrt(D)
+        s = np.where(keep, s, -np.inf)
+        m = s.max(-1)
+        out[b] = m + np.log(np.exp(s - m[..., None]).sum(-1))
+    return out
+
+
+def attention_bench(args):
+    cfg = CONFIGS[args.config]
+    B, T, C, H = cfg["B"], cfg["T"], cfg["C"], cfg["H"]
+    D = C // H
+    fwd_only = bool(cfg.get("forward_only"))
+    lib = gptc.load()
+    rt = gptc.Runtime(lib)
+    rt.init()
+    hip = Hip()
+    stream = rt.stream()
+
+    x = rt.normal((B, T, 3 * C), SEED_X)
+    dy = rt.normal((B, T, C), SEED_DY)
+    xt = rt.from_numpy(x)
+    dyt = rt.from_numpy(dy)
+    mask = rt.from_numpy(np.tril(np.ones((T, T), np.float32)))
+    # Compact cache layout of the library's Attention(): cache[0] is the input
+    # itself, cache[3] the 1-D backward state (probability blocks and maxima).
+    n_state = lib.gptc_attention_state_floats(B, T, C, H)
+
+    def make_set(xin):
+        return (gptc.TensorP * 4)(xin, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((n_state,))), \
+            rt.empty((B, T, C))
+
+    caches, yt = make_set(xt)
+    dqkv = rt.empty((B, T, 3 * C))
+    rt.sync()
+
+    def fwd(c=caches, y=yt):
+        lib.attention_forward_cuda_kernel(c[0], mask, H, c, y)
+
+    def step():
+        fwd()
+        lib.attention_backward_cuda_kernel(dyt, caches, H, dqkv)
+
+    def timed(fn, n):
+        """ms per call of n back-to-back calls between two events on the library stream."""
+        a, b = hip.event(), hip.event()
+        hip.record(a, stream)
+        for i in range(n):
+            fn(i)
+        hip.record(b, stream)
+        return hip.elapsed_ms(a, b) / n
+
+    log(f"[bench] {cfg['workload']}: B={B} T={T} H={H} D={D}; warmup {args.warmup}, steps {args.steps}")
+    for _ in range(args.warmup):
+        step()
+    rt.sync()
+    hip.device_sync()
+
+    # Headline: exactly K fwd+bwd steps between two events, nothing else on the stream.
+    ms_step = timed(lambda i: step(), args.steps)
+    rt.sync()
+    hip.device_sync()
+    # The same K-step measurement repeated, for the spread.
+    reps = [timed(lambda i: step(), args.steps) for _ in range(args.reps)]
+
+    # Per-kernel durations: K more steps with events recorded by the entry points
+    # around every kernel launch (each boundary then carries an event).
+    kernels = ("fwd", "bwd_delta", "bwd_dkdv", "bwd_dq")
+    k_ms = None
+    if not args.no_kernel_pass:
+        n_ev = 2 * len(kernels)
+        evs = [[hip.event() for _ in range(n_ev)] for _ in range(args.steps)]
+        ev_arrays = [(ctypes.c_void_p * n_ev)(*e) for e in evs]
+        for i in range(args.steps):
+            lib.gptc_set_kernel_events(ev_arrays[i], n_ev)
+            step()
+        rt.sync()
+        hip.device_sync()
+        lib.gptc_set_kernel_events(None, 0)
+        k_ms = {name: statistics.median(hip.elapsed_ms(e[2 * j], e[2 * j + 1]) for e in evs)
+                for j, name in enumerate(kernels)}
+
+    # The layer API as SelfAttention calls it (attn->forward / attn->backward
+    # through Attention()'s function pointers), allocation of the caches, y
+    # and dqkv included; the fresh input copies the layer takes ownership of
+    # are made outside the event pairs.
+    layer = gptc.AttentionLayer(rt, C, H, T)
+    layer.to(gptc.CUDA)
+    api_f, api_b = [], []
+    for i in range(args.warmup + args.steps):
+        xi, di = rt.empty((B, T, 3 * C)), rt.empty((B, T, C))
+        lib.tensor_copy(xi, xt)
+        lib.tensor_copy(di, dyt)
+        e = [hip.event() for _ in range(4)]
+        hip.record(e[0], stream)
+        yi = layer.forward(xi)
+        hip.record(e[1], stream)
+        rt.free(yi)
+        hip.record(e[2], stream)
+        gi = layer.backward(di)
+        hip.record(e[3], stream)
+        rt.free(gi)
+        if i >= args.warmup:
+            api_f.append(hip.elapsed_ms(e[0], e[1]))
+            api_b.append(hip.elapsed_ms(e[2], e[3]))
+    layer.free()
+    rt.sync()
+
+    # Forward alone, warm (one input, resident in the 256 MB MALL) and cold
+    # (rotating over enough input sets that every forward's inputs were
+    # evicted by the others' traffic).
+    ms_fwd_warm = timed(lambda i: fwd(), args.steps)
+    set_bytes = 4 * (B * T * 3 * C + 2 * B * T * C + B * H * T + n_state)
+    n_sets = max(3, int(np.ceil(2 * 256e6 / set_bytes)) + 1)
+    cold = [make_set(rt.from_numpy(x)) for _ in range(n_sets)] if n_sets * set_bytes < 8e9 else []
+    ms_fwd_cold = None
+    if cold:
+        for c, y in cold:
+            fwd(c, y)
+        rt.sync()
+        ms_fwd_cold = timed(lambda i: fwd(*cold[i % n_sets]), max(args.steps, 2 * n_sets))
+        rt.sync()
+        for c, y in cold:
+            for t in (*c, y):
+                rt.free(t)
+    step()  # leave the headline buffers with one fwd+bwd of the seeded inputs
+    rt.sync()
+
+    unit = contraction_flops(B, T, H, D)
+    peak, cu, mhz, peak_src = device_peak()
+    fwd_bytes, bwd_bytes = compulsory_bytes(B, T, C, H)
+    value_tflops = 6 * unit / (ms_step * 1e-3) / 1e12
+    fwd_cold_gbs = fwd_bytes / (ms_fwd_cold * 1e-3) / 1e9 if ms_fwd_cold else None
+    log(f"[bench] {ms_step:.4f} ms/step, {value_tflops:.2f} TFLOP/s; forward warm {ms_fwd_warm * 1e3:.2f} us, "
+        f"cold {ms_fwd_cold and ms_fwd_cold * 1e3:.2f} us; kernels (ms): {k_ms}")
+
+    result = {
+        "metric": attention_metric(cfg),
+        "value": round(fwd_cold_gbs, 1) if fwd_only else round(value_tflops, 3),
+        "unit": "GB/s" if fwd_only else "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_fwd_cold if fwd_only else ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": f"synthetic: qkv ~ N(0,1) seed {SEED_X}, dout ~ N(0,1) seed {SEED_DY} (torch-identical mt19937)",
+        "config": {"workload": cfg["workload"], "B": B, "T": T, "H": H, "D": D, "C": C,
+                   "causal_flop_per_step": (2 if fwd_only else 6) * unit},
+        "fwd_bwd": {
+            "ms_per_step": round(ms_step, 5),
+            "tflops": round(value_tflops, 3),
+            "pct_fp32_mfma_peak": round(100.0 * value_tflops / peak, 2),
+            "reps_ms_per_step": {"n": len(reps), "median": round(statistics.median(reps), 5),
+                                 "min": round(min(reps), 5), "max": round(max(reps), 5)},
+            # FlashAttention's convention (full T^2 work, backward 2.5x forward), for comparison only.
+            "tflops_fa_convention": round(7.0 * B * H * T * T * D / (ms_step * 1e-3) / 1e12, 3),
+            "compulsory_gb_per_s": round((fwd_bytes + bwd_bytes) / (ms_step * 1e-3) / 1e9, 1),
+            "tokens_per_s": round(B * T / (ms_step * 1e-3), 1),
+        },
+        "forward": {
+            "us_warm": round(ms_fwd_warm * 1e3, 3),
+            "us_cold": ms_fwd_cold and round(ms_fwd_cold * 1e3, 3),
+            "cold_input_sets": n_sets if cold else 0,
+            "compulsory_bytes": fwd_bytes,
+            "gb_per_s_warm": round(fwd_bytes / (ms_fwd_warm * 1e-3) / 1e9, 1),
+            "gb_per_s_cold": fwd_cold_gbs and round(fwd_cold_gbs, 1),
+            "tflops_warm": round(2 * unit / (ms_fwd_warm * 1e-3) / 1e12, 3),
+        },
+        "api_ms": {"forward_median": round(statistics.median(api_f), 5),
+                   "backward_median": round(statistics.median(api_b), 5),
+                   "step_median": round(statistics.median(a + b for a, b in zip(api_f, api_b)), 5),
+                   "note": "attn->forward / attn->backward through Attention(), allocation included"},
+        "peak_tflops": round(peak, 2),
+        "peak_source": f"{peak_src}: {cu} CU x {mhz} MHz x {FLOP_PER_CLK_CU_FP32_MFMA} flop/clk/CU",
+        "kernel_ms": k_ms and {k: round(v, 5) for k, v in k_ms.items()},
+    }
+    if fwd_only:
+        result["pct_hbm_peak"] = round(100.0 * fwd_cold_gbs / HBM_PEAK_GBS, 2)
+    else:
+        result["pct_fp32_mfma_peak"] = round(100.0 * value_tflops / peak, 2)
+        result["tflops_fa_convention"] = result["fwd_bwd"]["tflops_fa_convention"]
+        result["tokens_per_s"] = result["fwd_bwd"]["tokens_per_s"]
+
+    # Roofline of the dominant kernel: algorithmic work of one launch over its
+    # median duration in the per-kernel pass.  Contractions per kernel: forward
+    # S and PV; dk/dv kernel dP, dV, dK; dq kernel dQ (delta does none).
+    if k_ms:
+        kernel_flops = {"fwd": 2 * unit, "bwd_delta": 0.0, "bwd_dkdv": 3 * unit, "bwd_dq": 1 * unit}
+        symbols = {"fwd": ("attn_fwd16_kernel", "attn_fwd_kernel"), "bwd_delta": ("attn_bwd_delta_kernel",),
+                   "bwd_dkdv": ("attn_bwd_dkdv_kernel",), "bwd_dq": ("attn_bwd_dq16_kernel", "attn_bwd_dq_kernel")}
+        dom = "fwd" if fwd_only else max(k_ms, key=k_ms.get)
+        if fwd_only:
+            achieved = fwd_bytes / (k_ms[dom] * 1e-3) / 1e9
+            roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "algorithmic_bytes_per_launch": fwd_bytes}
+        else:
+            achieved = kernel_flops[dom] / (k_ms[dom] * 1e-3) / 1e12
+            roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": round(peak, 2),
+                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                    "algorithmic_flop_per_launch": kernel_flops[dom]}
+        roof["duration_ms"] = round(k_ms[dom], 5)
+        # HBM bytes per launch from the committed rocprof byte-counter runs
+        # (FETCH_SIZE and WRITE_SIZE, scaled by a plain copy of known size).
+        traffic_file = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.config}.json")
+        sym = symbols[dom][0] if D == 64 else symbols[dom][-1]
+        if os.path.exists(traffic_file):
+            with open(traffic_file) as fh:
+                tr = json.load(fh)
+            k = tr["kernels"].get(sym)
+            if k:
+                roof["traffic"] = k["read_bytes"] + k["write_bytes"]
+                roof["traffic_source"] = (f"profiles/hbm_traffic_{args.config}.json (rocprofv3 FETCH_SIZE "
+                                          f"x{tr['fetch_scale']:.2f} + WRITE_SIZE x{tr['write_scale']:.2f})")
+        result["roofline"] = roof
+
+    gpu_out = None
+    if not args.no_cpu_baseline:
+        gpu_out = {"y": rt.to_numpy(yt), "lse": rt.to_numpy(caches[2]).reshape(B, H, T),
+                   "dqkv": None if fwd_only else rt.to_numpy(dqkv)}
+    for t in (dyt, mask, yt, dqkv, *caches):
+        rt.free(t)
+    rt.sync()
+
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle over OpenBLAS) ...")
+        cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s, gpu_out)
+        result["cpu_baseline"] = {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cb.items()}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -480,6 +728,10 @@ def main():
                          "c4: C4 greedy generation with GPT-2 124M")
     ap.add_argument("--c4-loops", default="eager,graph,window",
                     help="c4 workload: the loops to time (comma list of eager, graph, window)")
+    ap.add_argument("--reps", type=int, default=10,
+                    help="attention: repetitions of the K-step timing after the headline (median/min)")
+    ap.add_argument("--no-kernel-pass", action="store_true",
+                    help="attention: skip the per-kernel event pass (e.g. under a kernel trace of the headline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
@@ -501,138 +753,7 @@ def main():
         copy_calibration(args)
         return
 
-    cfg = CONFIGS[args.config]
-    B, T, C, H = cfg["B"], cfg["T"], cfg["C"], cfg["H"]
-    D = C // H
-    lib = gptc.load()
-    rt = gptc.Runtime(lib)
-    rt.init()
-    hip = Hip()
-    stream = rt.stream()
-
-    x = rt.normal((B, T, 3 * C), SEED_X)
-    dy = rt.normal((B, T, C), SEED_DY)
-    xt = rt.from_numpy(x)
-    dyt = rt.from_numpy(dy)
-    mask = rt.from_numpy(np.tril(np.ones((T, T), np.float32)))
-    # Compact cache layout of the library's Attention(): cache[0] is the input
-    # itself, cache[3] the 1-D backward state (probability blocks and maxima).
-    n_state = lib.gptc_attention_state_floats(B, T, C, H)
-    caches = (gptc.TensorP * 4)(xt, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((n_state,)))
-    yt = rt.empty((B, T, C))
-    dqkv = rt.empty((B, T, 3 * C))
-    rt.sync()
-
-    def step():
-        lib.attention_forward_cuda_kernel(xt, mask, H, caches, yt)
-        lib.attention_backward_cuda_kernel(dyt, caches, H, dqkv)
-
-    log(f"[bench] {cfg['workload']}: B={B} T={T} H={H} D={D}; warmup {args.warmup}, steps {args.steps}")
-    for _ in range(args.warmup):
-        step()
-    rt.sync()
-    hip.device_sync()
-
-    # Timed region: exactly K steps, nothing else on the stream.
-    t_begin, t_end = hip.event(), hip.event()
-    hip.record(t_begin, stream)
-    for _ in range(args.steps):
-        step()
-    hip.record(t_end, stream)
-    rt.sync()
-    hip.device_sync()
-    total_ms = hip.elapsed_ms(t_begin, t_end)
-    ms_per_step = total_ms / args.steps
-
-    # Per-kernel breakdown (for the roofline): the same K steps once more, with
-    # events recorded on the library stream around every kernel launch.
-    kernels = ("fwd", "bwd_delta", "bwd_dkdv", "bwd_dq")
-    n_ev = 2 * len(kernels)
-    evs = [[hip.event() for _ in range(n_ev)] for _ in range(args.steps)]
-    ev_arrays = [(ctypes.c_void_p * n_ev)(*e) for e in evs]
-    for i in range(args.steps):
-        lib.gptc_set_kernel_events(ev_arrays[i], n_ev)
-        step()
-    rt.sync()
-    hip.device_sync()
-    lib.gptc_set_kernel_events(None, 0)
-    k_ms = {name: statistics.mean(hip.elapsed_ms(e[2 * j], e[2 * j + 1]) for e in evs)
-            for j, name in enumerate(kernels)}
-
-    unit = contraction_flops(B, T, H, D)
-    flops = 6 * unit
-    peak, cu, mhz, peak_src = device_peak()
-    value = flops / (ms_per_step * 1e-3) / 1e12
-    # Algorithmic contractions per kernel: forward S and PV; dk/dv kernel dP,
-    # dV, dK; dq kernel dQ (the delta kernel does no contraction).
-    kernel_flops = {"fwd": 2 * unit, "bwd_delta": 0.0, "bwd_dkdv": 3 * unit, "bwd_dq": 1 * unit}
-    dom = max(k_ms, key=k_ms.get)
-    achieved = kernel_flops[dom] / (k_ms[dom] * 1e-3) / 1e12
-    log(f"[bench] {ms_per_step:.4f} ms/step, {value:.2f} TFLOP/s; kernels (ms): " +
-        ", ".join(f"{k} {v:.4f}" for k, v in k_ms.items()))
-
-    result = {
-        "metric": METRIC,
-        "value": round(value, 3),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp32",
-        "data": f"synthetic: qkv ~ N(0,1) seed {SEED_X}, dout ~ N(0,1) seed {SEED_DY} (torch-identical mt19937)",
-        "config": {"workload": cfg["workload"], "B": B, "T": T, "H": H, "D": D, "C": C,
-                   "causal_flop_per_step": flops},
-        "pct_fp32_mfma_peak": round(100.0 * value / peak, 2),
-        # FlashAttention's convention (full T^2 work, backward 2.5x forward), for comparison only.
-        "tflops_fa_convention": round(7.0 * B * H * T * T * D / (ms_per_step * 1e-3) / 1e12, 3),
-        # Compulsory HBM bytes: forward reads qkv, writes y and LSE; backward reads qkv, y, dy and LSE, writes dqkv.
-        "compulsory_gb_per_s": round(4.0 * (B * T * (3 * C + C) + B * H * T + B * T * (3 * C + 2 * C) + B * H * T +
-                                            B * T * 3 * C) / (ms_per_step * 1e-3) / 1e9, 1),
-        "tokens_per_s": round(B * T / (ms_per_step * 1e-3), 1),
-        "peak_tflops": round(peak, 2),
-        "peak_source": f"{peak_src}: {cu} CU x {mhz} MHz x {FLOP_PER_CLK_CU_FP32_MFMA} flop/clk/CU",
-        "kernel_ms": {k: round(v, 5) for k, v in k_ms.items()},
-        "roofline": {
-            "kernel": dom,
-            "bound": "mfma",
-            "achieved": round(achieved, 3),
-            "peak": round(peak, 2),
-            "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4),
-            "traffic": None,
-            "algorithmic_flop_per_launch": kernel_flops[dom],
-        },
-    }
-    # HBM bytes per launch of the dominant kernel, from the committed rocprof
-    # byte-counter runs (scaled by a plain copy; see profiles/).
-    traffic_file = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.config}.json")
-    # D = 64 runs the 16-row forward and dq kernels; other head sizes the 32-row ones.
-    kernel_symbols = {"fwd": ("attn_fwd16_kernel", "attn_fwd_kernel"), "bwd_delta": ("attn_bwd_delta_kernel",),
-                      "bwd_dkdv": ("attn_bwd_dkdv_kernel",),
-                      "bwd_dq": ("attn_bwd_dq16_kernel", "attn_bwd_dq_kernel")}[dom]
-    kernel_symbol = kernel_symbols[0] if D == 64 else kernel_symbols[-1]
-    if os.path.exists(traffic_file):
-        with open(traffic_file) as f:
-            tr = json.load(f)["kernels"].get(kernel_symbol)
-        if tr:
-            result["roofline"]["traffic"] = tr["read_bytes"] + tr["write_bytes"]
-            result["roofline"]["traffic_source"] = f"profiles/hbm_traffic_{args.config}.json (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE)"
-    gpu_out = None if args.no_cpu_baseline else (rt.to_numpy(yt), rt.to_numpy(dqkv))
-    for t in (dyt, mask, yt, dqkv, *caches):
-        rt.free(t)
-    rt.sync()
-
-    if not args.no_cpu_baseline:
-        log("[bench] CPU baseline (oracle over OpenBLAS) ...")
-        cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s, gpu_out)
-        result["cpu_baseline"] = {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cb.items()}
-    else:
-        result["cpu_baseline"] = None
-    print(json.dumps(result), flush=True)
+    attention_bench(args)
 
 
 if __name__ == "__main__":

@@ -510,9 +510,10 @@ size_t bwd_ds_floats(int B, int H, int T) {
 
 void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     BwdParams p = p_in;
-    if (p.vec)
+    // The grid order serves the 32-row dq kernel only (the 16-row one pairs blocks).
+    if (!p.full && p.vec)
         p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<true, false>);
-    else
+    else if (!p.full)
         p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<false, false>);
     const dim3 block(256);
     const int rows = p.B * p.T * p.H;

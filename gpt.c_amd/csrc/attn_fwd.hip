@@ -468,11 +468,9 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
         if (ev) hipCheck(hipEventRecord(ev[1], stream));
         return;
     }
-    if (p.full && perm)
-        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, true, true>);
-    else if (p.full)
-        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, true, false>);
-    else if (p.vec && perm)
+    // The 32-row kernel: other head sizes and unaligned rows (FULL is the
+    // 16-row kernel's case above).
+    if (p.vec && perm)
         p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, false, true>);
     else if (p.vec)
         p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, false, false>);
@@ -483,11 +481,7 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
     const dim3 grid(p.nqb * p.bh_pad), block(256);
     const bool vec = p.vec;
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
-    if (p.full && perm)
-        attn_fwd_kernel<true, true, true><<<grid, block, 0, stream>>>(p);
-    else if (p.full)
-        attn_fwd_kernel<true, true, false><<<grid, block, 0, stream>>>(p);
-    else if (vec && perm)
+    if (vec && perm)
         attn_fwd_kernel<true, false, true><<<grid, block, 0, stream>>>(p);
     else if (vec)
         attn_fwd_kernel<true, false, false><<<grid, block, 0, stream>>>(p);

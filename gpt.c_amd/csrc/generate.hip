@@ -14,7 +14,9 @@
 // (gptc_gpt2_generate) captures one step as a HIP graph with the position in
 // device memory and replays it, instead of launching and waiting per token.
 #include <hip/hip_runtime.h>
+#include <cstdint>
 #include <cstdlib>
+#include <cstring>
 #include "generate.h"
 #include "gpu_kernels.h"
 #include "ops_common.hpp"
@@ -49,7 +51,8 @@ void step_body(gpt2_t *gpt, gptc_kv_cache_t *kv, int pos, const int *pos_dev, te
 }
 
 void check_model(const gpt2_t *gpt, const gptc_kv_cache_t *kv) {
-    CHECK_ERROR(gpt == NULL || kv == NULL, "Expected a model and a KV cache, but got NULL.");
+    REQUIRE_ARG(gpt);
+    REQUIRE_ARG(kv);
     CHECK_ERROR(gpt->wte->W->device != CUDA, "Generation runs on the GPU: move the model there first.");
     CHECK_ERROR(kv->n_layers != gpt->n_layers, "The cache was made for %d layers, the model has %d.", kv->n_layers,
                 gpt->n_layers);
@@ -58,13 +61,50 @@ void check_model(const gpt2_t *gpt, const gptc_kv_cache_t *kv) {
 void drop_graph(gptc_kv_cache_t *kv) {
     if (kv->graph_exec != nullptr) hipCheck(hipGraphExecDestroy(static_cast<hipGraphExec_t>(kv->graph_exec)));
     kv->graph_exec = nullptr;
-    kv->graph_tokens = nullptr;
+    free(kv->graph_key);
+    kv->graph_key = nullptr;
+    kv->graph_key_len = 0;
+}
+
+// Every value the captured step's launches take as an argument and that a
+// caller can change between calls: the model object, each parameter's
+// device address, the LayerNorm eps values, the shapes, the token buffer,
+// prompt and total.  (The cache's own buffers are fixed for its lifetime.)
+// Returns a malloc'd array of *len words.
+unsigned long long *graph_key(const gpt2_t *gpt, const tensor_t *tokens, int prompt, int total, int *len) {
+    const int np = gpt->_num_param_tensors;
+    const int n = 8 + np + 2 * gpt->n_layers + 1;
+    auto *key = static_cast<unsigned long long *>(mallocCheck(sizeof(unsigned long long) * n));
+    int i = 0;
+    auto bits = [](float f) {
+        unsigned u;
+        memcpy(&u, &f, sizeof(u));
+        return static_cast<unsigned long long>(u);
+    };
+    key[i++] = reinterpret_cast<uintptr_t>(gpt);
+    key[i++] = reinterpret_cast<uintptr_t>(tokens->t);
+    key[i++] = static_cast<unsigned long long>(prompt);
+    key[i++] = static_cast<unsigned long long>(total);
+    key[i++] = static_cast<unsigned long long>(gpt->n_heads);
+    key[i++] = static_cast<unsigned long long>(gpt->n_embd);
+    key[i++] = static_cast<unsigned long long>(gpt->vocab_size);
+    key[i++] = static_cast<unsigned long long>(np);
+    tensor_t **params = gpt->parameters(gpt);
+    for (int p = 0; p < np; p++) key[i++] = reinterpret_cast<uintptr_t>(params[p]->t);
+    free(params);
+    for (int l = 0; l < gpt->n_layers; l++) {
+        key[i++] = bits(gpt->layers[l]->ln1->eps);
+        key[i++] = bits(gpt->layers[l]->ln2->eps);
+    }
+    key[i++] = bits(gpt->ln_f->eps);
+    *len = i;
+    return key;
 }
 
 }  // namespace
 
 extern "C" gptc_kv_cache_t *gptc_kv_cache_create(const gpt2_t *gpt, const int B, const int L) {
-    CHECK_ERROR(gpt == NULL, "Expected *gpt to be a gpt2_t pointer, but got NULL.");
+    REQUIRE_ARG(gpt);
     CHECK_ERROR(B < 1 || B > 8, "The decode step takes 1 .. 8 sequences, but got B = %d.", B);
     CHECK_ERROR(L < 1 || L > gpt->block_size, "Expected 1 <= L <= block_size = %d, but got L = %d.", gpt->block_size,
                 L);
@@ -95,8 +135,8 @@ extern "C" gptc_kv_cache_t *gptc_kv_cache_create(const gpt2_t *gpt, const int B,
     kv->logits = create_tensor(s_bv, 3, CUDA);
     kv->pos_dev = static_cast<int *>(alloc_cuda(sizeof(int)));
     kv->graph_exec = nullptr;
-    kv->graph_tokens = nullptr;
-    kv->graph_prompt = kv->graph_total = 0;
+    kv->graph_key = nullptr;
+    kv->graph_key_len = 0;
     return kv;
 }
 
@@ -137,9 +177,13 @@ extern "C" void gptc_gpt2_generate(gpt2_t *gpt, gptc_kv_cache_t *kv, tensor_t *t
                 "Expected 1 <= prompt <= total <= L = %d, but got prompt %d, total %d.", kv->L, prompt, total);
     if (total == prompt) return;  // nothing to generate
     hipStream_t s = gptc_stream_checked();
-    const bool reuse = kv->graph_exec != nullptr && kv->graph_tokens == tokens->t && kv->graph_prompt == prompt &&
-                       kv->graph_total == total;
-    if (!reuse) {
+    int key_len = 0;
+    unsigned long long *key = graph_key(gpt, tokens, prompt, total, &key_len);
+    const bool reuse = kv->graph_exec != nullptr && kv->graph_key_len == key_len &&
+                       memcmp(kv->graph_key, key, sizeof(unsigned long long) * key_len) == 0;
+    if (reuse) {
+        free(key);
+    } else {
         drop_graph(kv);
         // The captured step: every launch reads the position from kv->pos_dev.
         hipGraph_t graph;
@@ -153,9 +197,8 @@ extern "C" void gptc_gpt2_generate(gpt2_t *gpt, gptc_kv_cache_t *kv, tensor_t *t
         hipCheck(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
         hipCheck(hipGraphDestroy(graph));
         kv->graph_exec = exec;
-        kv->graph_tokens = tokens->t;
-        kv->graph_prompt = prompt;
-        kv->graph_total = total;
+        kv->graph_key = key;
+        kv->graph_key_len = key_len;
     }
     // Position 0, then one replay per position 0 .. total-2 (each reads the
     // token at pos and writes the token at pos + 1 once past the prompt).

@@ -22,6 +22,7 @@
 #include <array>
 #include <climits>
 #include <map>
+#include <utility>
 
 #include "hip_check.hpp"
 
@@ -54,20 +55,23 @@ __device__ __forceinline__ void grid_position(const GridOrder &o, int nblk, int 
 // the co-resident rounds (ties: the largest smallest sum).  Cached per shape.
 template <typename Kernel>
 GridOrder choose_grid_order(int nblk, int bh_pad, Kernel kernel) {
-    // Device properties and the kernel's occupancy, once per device (this
-    // runs on every launch, so no runtime queries after the first).
+    // Device properties and the kernel's occupancy, once per device and
+    // kernel (this runs on every launch, so no runtime queries after the
+    // first).  Keyed on the kernel's address: template variants of a kernel
+    // share one function type but not their register counts.
     struct DeviceInfo {
         int cus_total, per_cu;
     };
-    static std::map<int, DeviceInfo> devices;
+    static std::map<std::pair<int, const void *>, DeviceInfo> devices;
     int dev = 0;
     hipCheck(hipGetDevice(&dev));
-    auto d = devices.find(dev);
+    const std::pair<int, const void *> dkey{dev, reinterpret_cast<const void *>(kernel)};
+    auto d = devices.find(dkey);
     if (d == devices.end()) {
         DeviceInfo info{};
         hipCheck(hipDeviceGetAttribute(&info.cus_total, hipDeviceAttributeMultiprocessorCount, dev));
         hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&info.per_cu, kernel, 256, 0));
-        d = devices.emplace(dev, info).first;
+        d = devices.emplace(dkey, info).first;
     }
     GridOrder o{};
     const int cus_total = d->second.cus_total, per_cu = d->second.per_cu;

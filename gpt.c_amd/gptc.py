@@ -468,6 +468,34 @@ class GPT2Model(_Layer):
         """gptc_save_model(path, model, steps)."""
         self.rt.lib.gptc_save_model(os.fsencode(path), self.raw, steps)
 
+    # Per-block parameters in the order block_t's parameters() lists them
+    # (ln1, attention qkv and c_proj, ln2, MLP c_fc and c_proj; weight, bias).
+    BLOCK_PARAMS = ("ln1.W", "ln1.b", "qkv.W", "qkv.b", "attn_proj.W", "attn_proj.b",
+                    "ln2.W", "ln2.b", "fc.W", "fc.b", "mlp_proj.W", "mlp_proj.b")
+
+    def param_layout(self):
+        """(name, shape) of every parameter in parameters() order, the shapes
+        read from the model's own tensors."""
+        names = ["wte", "wpe"] + [f"h{i}.{n}" for i in range(self.s.n_layers) for n in self.BLOCK_PARAMS] + \
+            ["ln_f.W", "ln_f.b"]
+        ts = self.parameters()
+        assert len(ts) == len(names), (len(ts), len(names))
+        return [(n, tuple(t.contents.shape[:t.contents.ndims])) for n, t in zip(names, ts)]
+
+    def random_init_arrays(self, seed_base=1000, std=0.02):
+        """The random init of BASELINE's GPT-2 configs: every matrix and
+        embedding N(0, std) from seed seed_base + its index in parameters()
+        order, biases 0, LayerNorm weights 1.  Returns the host arrays."""
+        out = []
+        for i, (name, shp) in enumerate(self.param_layout()):
+            if name.endswith(("ln1.W", "ln2.W")) or name == "ln_f.W":
+                out.append(np.ones(shp, np.float32))
+            elif len(shp) == 1:
+                out.append(np.zeros(shp, np.float32))
+            else:
+                out.append(self.rt.normal(shp, seed_base + i, 0.0, std))
+        return out
+
     def fast_load(self, arrays):
         """fast_load_state_dict from numpy arrays in parameters() order."""
         ts = [self.rt.from_numpy(a, CPU) for a in arrays]

@@ -27,7 +27,14 @@
  *                                   and replayed, the position living in
  *                                   device memory, so the host does not wait
  *                                   between tokens.  Returns without
- *                                   synchronising; total <= L.
+ *                                   synchronising; total <= L.  The graph
+ *                                   is reused by a later call only when the
+ *                                   model object, the address of every
+ *                                   parameter, the token buffer, prompt,
+ *                                   total and the LayerNorm eps values are
+ *                                   all unchanged; otherwise it is captured
+ *                                   again (a model moved between devices
+ *                                   has new addresses).
  * gptc_kv_cache_free(kv)
  */
 #pragma once
@@ -49,9 +56,9 @@ typedef struct gptc_kv_cache {
     tensor_t *logits;      // (B, 1, V) of the captured step
     int *pos_dev;          // device-side position of the captured step
     void *graph_exec;      // hipGraphExec_t of the captured step
-    const float *graph_tokens;
-    int graph_prompt;
-    int graph_total;
+    unsigned long long *graph_key;  // everything the captured launches baked in
+    int graph_key_len;              // (model and buffer addresses, shapes, eps):
+                                    // the graph is replayed only on an exact match
 } gptc_kv_cache_t;
 
 gptc_kv_cache_t *gptc_kv_cache_create(const gpt2_t *gpt, const int B, const int L);

@@ -133,6 +133,64 @@ def test_tokenizer_decodes(rt, tmp_path):
     ctypes.CFUNCTYPE(None, ctypes.c_void_p)(tk.free_layer)(raw)
 
 
+def test_dataloader_reset_and_ragged_file(rt, tmp_path):
+    """A file whose size is not a whole number of ids (a trailing partial id)
+    and reset(): windows restart at id 0, len() counts whole windows."""
+    B, T = 2, 3
+    toks = np.arange(7, 7 + 20, dtype=np.int32)
+    path = tmp_path / "ragged.bin"
+    path.write_bytes(toks.tobytes() + b"\x01\x02")  # 82 bytes
+    raw = rt.lib.DataLoader(os.fsencode(path), B, T)
+    dl = ctypes.cast(raw, ctypes.POINTER(DataLoaderT)).contents
+    nxt = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.POINTER(gptc.TensorP))(dl.next)
+    assert ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)(dl.len)(raw) == 82 // (4 * (B * T + 1))
+    batch = (gptc.TensorP * 2)()
+    starts = []
+    for i in range(5):
+        if i == 3:
+            ctypes.CFUNCTYPE(None, ctypes.c_void_p)(dl.reset)(raw)
+        nxt(raw, batch)
+        x, y = rt.to_numpy(batch[0]).ravel(), rt.to_numpy(batch[1]).ravel()
+        s0 = int(x[0]) - 7
+        assert np.array_equal(x, toks[s0:s0 + B * T].astype(np.float32))
+        assert np.array_equal(y, toks[s0 + 1:s0 + B * T + 1].astype(np.float32))
+        starts.append(s0)
+        rt.free(batch[0])
+        rt.free(batch[1])
+    # 20 whole ids: windows of 7 at 0, 6, 12 (needs ids 12..18), then 18 would
+    # need 18..24: wrap to 0; reset before the 4th call restarts at 0 too.
+    assert starts == [0, 6, 12, 0, 6]
+    ctypes.CFUNCTYPE(None, ctypes.c_void_p)(dl.free_layer)(raw)
+
+
+@pytest.mark.parametrize("case", ["too_small", "bad_magic", "truncated_piece", "empty_piece"])
+def test_format_errors_are_fatal(tmp_path, case):
+    """Malformed inputs end the process with the library's error, never a
+    read past the data."""
+    path = tmp_path / "f.bin"
+    if case == "too_small":
+        np.arange(6, dtype=np.int32).tofile(path)  # one window needs 2*3+1 = 7 ids
+        call = f"lib.DataLoader({os.fsencode(path)!r}, 2, 3)"
+    else:
+        header = np.zeros(256, np.int32)
+        header[:3] = [20240415 if case != "bad_magic" else 1234, 2, 1]
+        body = {"bad_magic": b"\x01a\x01b", "truncated_piece": b"\x01a\x05bc", "empty_piece": b"\x01a\x00"}[case]
+        path.write_bytes(header.tobytes() + body)
+        call = f"lib.Tokenizer({os.fsencode(path)!r})"
+    code = textwrap.dedent(f"""
+        import sys
+        sys.path.insert(0, {os.path.join(ROOT, 'gpt.c_amd')!r})
+        import gptc
+        lib = gptc.load()
+        {call}
+    """)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "[ERROR]" in r.stderr, r.stderr
+    expect = {"too_small": "fewer than one window", "bad_magic": "not a tokenizer.bin",
+              "truncated_piece": "ends inside", "empty_piece": "empty byte string"}[case]
+    assert expect in r.stderr, r.stderr
+
+
 @pytest.mark.gpu
 def test_checkpoint_saved_from_gpu_round_trips(tmp_path):
     lib = gptc.load()
