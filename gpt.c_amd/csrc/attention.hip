@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdint>
 #include <initializer_list>
+#include <mutex>
 #include "attn_kernels.hpp"
 #include "ops_common.hpp"
 #include "gpu_kernels.h"
@@ -372,6 +373,64 @@ void decode_step(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, cons
 extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos,
                                              const int n_heads, tensor_t *output) {
     decode_step(qkv, k_cache, v_cache, pos, nullptr, n_heads, output, nullptr);
+}
+
+// ---- Allocation-free decode step ----
+// The split-key decode's partials (B*H*splits*kDecPartStride floats) live in
+// a file-scope device array instead of a stream-ordered allocation, for
+// callers that must not allocate (graph capture, serving loops).  Each GPU
+// holds its own copy of the array until the process ends; host code reaches
+// it only through the address hipGetSymbolAddress returns for the current
+// device (the array's name is a host-side stand-in, not a device address).
+// Every call on a GPU reuses that GPU's array: calls that overlap on one GPU
+// (other streams, other threads) race.  Nothing needs clearing between
+// calls: the merge kernel reads only the partials the split kernel of the
+// same call wrote.
+namespace {
+
+constexpr size_t kDecodeScratchFloats = size_t(1) << 20;  // 4 MiB per GPU
+__device__ __align__(256) float scratch[kDecodeScratchFloats];
+
+constexpr int kMaxDevices = 64;
+float *g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch`, looked up once per device.
+float *device_scratch() {
+    int dev = 0;
+    hipCheck(hipGetDevice(&dev));
+    CHECK_ERROR(dev < 0 || dev >= kMaxDevices, "Device %d is beyond the %d devices the decode scratch serves.", dev,
+                kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        CHECK_ERROR(rc != hipSuccess || p == nullptr, "hipGetSymbolAddress(decode scratch) failed on device %d: %s.",
+                    dev, hipGetErrorString(rc));
+        g_scratch_ptr[dev] = static_cast<float *>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" void attention_decode_noalloc_cuda_kernel(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache,
+                                                     const int pos, const int n_heads, tensor_t *output) {
+    gptc::DecParams p = decode_params(qkv, k_cache, v_cache, pos, nullptr, n_heads, output);
+    if (p.B == 0 || p.C == 0) return;
+    if (p.full) {
+        const size_t need = static_cast<size_t>(p.B) * p.H * p.splits * gptc::kDecPartStride;
+        CHECK_ERROR(need > kDecodeScratchFloats,
+                    "attention_decode_noalloc_cuda_kernel: B=%d, H=%d, pos=%d needs %zu floats of partials, more than "
+                    "its fixed %zu-float scratch; use attention_decode_cuda_kernel.",
+                    p.B, p.H, pos, need, kDecodeScratchFloats);
+        p.part = device_scratch();
+    }
+    gptc::launch_attn_decode(p, gptc_stream_checked());
+}
+
+extern "C" long long gptc_decode_noalloc_scratch_floats(void) {
+    return static_cast<long long>(kDecodeScratchFloats);
 }
 
 void gptc::attention_decode_devpos(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int *pos_dev,

@@ -157,6 +157,8 @@ SIGNATURES = {
     "gptc_set_kernel_events": (None, [ctypes.POINTER(_vp), _ci]),
     "gptc_attention_state_floats": (ctypes.c_longlong, [_ci, _ci, _ci, _ci]),
     "attention_decode_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
+    "attention_decode_noalloc_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
+    "gptc_decode_noalloc_scratch_floats": (ctypes.c_longlong, []),
     "saxpy_cuda": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),
     "sgemm_cuda": (None, [_ci, _ci, _ci, _ci, _ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci, _cf, TensorP, _ci,
                           _ci]),

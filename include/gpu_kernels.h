@@ -205,6 +205,28 @@ void attention_decode_cuda_kernel(
 );
 
 /*
+ * attention_decode_noalloc_cuda_kernel(qkv, k_cache, v_cache, pos, n_heads, output)
+ *   No counterpart in the reference.  For callers that cannot allocate
+ *   device memory (code under HIP graph capture, tight serving loops,
+ *   harnesses that forbid hipMalloc): the same step, arguments and results
+ *   as attention_decode_cuda_kernel, but its partial softmax states go to a
+ *   fixed device array (gptc_decode_noalloc_scratch_floats() floats, 4 MiB,
+ *   one per GPU, held until the process ends) instead of a stream-ordered
+ *   allocation; the call allocates and frees nothing.  A step needing more
+ *   partials (B*H*ceil((pos+1)/64)*68 floats) is a fatal error.  Calls that
+ *   overlap on one GPU share that array and race.
+ */
+void attention_decode_noalloc_cuda_kernel(
+    const tensor_t *qkv,
+    tensor_t *k_cache,
+    tensor_t *v_cache,
+    const int pos,
+    const int n_heads,
+    tensor_t *output
+);
+long long gptc_decode_noalloc_scratch_floats(void);
+
+/*
  * ---- extensions with no counterpart in the reference ----
  * gptc_stream(): the hipStream_t (as void*) every launch of this library is
  * ordered on; for callers that time or order their own work against it.
