@@ -533,6 +533,20 @@ def attention_bench(args):
         return hip.elapsed_ms(a, b) / n
 
     log(f"[bench] {cfg['workload']}: B={B} T={T} H={H} D={D}; warmup {args.warmup}, steps {args.steps}")
+    # Device pre-warm, untimed, before the W warm-up steps: a kernel trace of
+    # this bench shows the GPU's clocks settling over the first ~40 ms of
+    # sustained load (step time 0.53 -> 0.41 ms at C2), so a short warm-up
+    # would time the power-management ramp instead of the kernels.  Steps
+    # run until prewarm_ms of wall time have passed; the line reports it.
+    t_pre = time.perf_counter()
+    n_pre = 0
+    while (time.perf_counter() - t_pre) * 1e3 < args.prewarm_ms:
+        for _ in range(8):
+            step()
+        n_pre += 8
+        rt.sync()
+    prewarm = {"ms": round((time.perf_counter() - t_pre) * 1e3, 1), "steps": n_pre,
+               "reason": "untimed, before the W warm-up steps: lets the clocks settle under sustained load"}
     for _ in range(args.warmup):
         step()
     rt.sync()
@@ -623,6 +637,7 @@ def attention_bench(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm": prewarm,
         "ms_per_step": round(ms_fwd_cold if fwd_only else ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -635,8 +650,8 @@ def attention_bench(args):
             "ms_per_step": round(ms_step, 5),
             "tflops": round(value_tflops, 3),
             "pct_fp32_mfma_peak": round(100.0 * value_tflops / peak, 2),
-            "reps_ms_per_step": {"n": len(reps), "median": round(statistics.median(reps), 5),
-                                 "min": round(min(reps), 5), "max": round(max(reps), 5)},
+            "reps_ms_per_step": reps and {"n": len(reps), "median": round(statistics.median(reps), 5),
+                                          "min": round(min(reps), 5), "max": round(max(reps), 5)},
             # FlashAttention's convention (full T^2 work, backward 2.5x forward), for comparison only.
             "tflops_fa_convention": round(7.0 * B * H * T * T * D / (ms_step * 1e-3) / 1e12, 3),
             "compulsory_gb_per_s": round((fwd_bytes + bwd_bytes) / (ms_step * 1e-3) / 1e9, 1),
@@ -730,6 +745,8 @@ def main():
                     help="c4 workload: the loops to time (comma list of eager, graph, window)")
     ap.add_argument("--reps", type=int, default=10,
                     help="attention: repetitions of the K-step timing after the headline (median/min)")
+    ap.add_argument("--prewarm-ms", type=float, default=300.0,
+                    help="attention: untimed steps for this long (wall ms) before the W warm-up steps")
     ap.add_argument("--no-kernel-pass", action="store_true",
                     help="attention: skip the per-kernel event pass (e.g. under a kernel trace of the headline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -152,6 +152,30 @@ def test_graph_generation_matches_eager_steps(rt):
     print(f"  {3 * (total - 5)} generated tokens agree; generated ids span {len(np.unique(eager[:, 5:]))} values")
 
 
+def test_graph_not_replayed_for_another_model(rt):
+    """One KV cache serving two models of the same shape, then the first model
+    moved to the CPU and back (new parameter addresses): every call must
+    capture or reuse a graph that reads the model it is given, so each call's
+    tokens equal the eager loop's for that model."""
+    V, block, L, H, C = 211, 64, 2, 4, 96
+    models = [make_model(rt, c3_params(V, block, L, C, seed=s, std=0.3, jitter=0.1), V, block, L, H, C)
+              for s in (21, 22)]
+    prompts = np.random.default_rng(7).integers(0, V, (2, 6))
+    total = 32
+    eager = [np.stack([kv_generate(rt, m, p, total, block)[0] for p in prompts]) for m in models]
+    assert not np.array_equal(eager[0], eager[1]), "the two models should generate different tokens"
+    cache = gptc.KVCache(rt, models[0], 2, total)
+    for i in (0, 1, 0, 1):
+        got = graph_generate(rt, models[i], prompts, total, cache)
+        assert np.array_equal(got, eager[i]), f"model {i}: tokens of a stale graph"
+    models[0].to(gptc.CPU)
+    models[0].to(gptc.CUDA)
+    assert np.array_equal(graph_generate(rt, models[0], prompts, total, cache), eager[0]), "after a device move"
+    cache.free()
+    for m in models:
+        m.free()
+
+
 def test_c4_greedy_generation(rt, oracle):
     """C4: GPT-2 124M, N(0, 0.02) init, B = 1, 64-token prompt, greedy to T = 512."""
     V, block, L, H, C = 50257, 1024, 12, 12, 768
