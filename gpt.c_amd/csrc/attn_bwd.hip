@@ -373,10 +373,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
         }
 }
 
-// ---- dQ, 16-row paired form (D == kDPad, 16-byte rows, 31-bit head sizes) ----
-// WG = 4 waves x 16 queries = one 64-query block j of one (b, h), then block
-// nqt-1-j of the same head, so every WG reduces nqt+1 key tiles and the grid
-// ((nqt+1)/2 x heads) is resident at once with equal work per WG.
+// ---- dQ, 16-row form (D == kDPad, 16-byte rows, 31-bit head sizes) ----
+// WG = 4 waves x 16 queries = one 64-query block of one (b, h) at a time,
+// running the blocks of its work list (block_sched.hpp: at B=8, H=12,
+// T=1024 blocks j and 15-j of one head, so every WG reduces nqt+1 key
+// tiles and the grid is resident at once with equal work per WG).
 // v_mfma_f32_16x16x4_f32 on dQ[q][d] += sum_k dS[q][k] K[k][d]:
 //   A = dS (lane l: query l%16, k-slot l/16), B = K (k-slot l/16, column l%16).
 // Step (t, c) of a 64-key tile puts key 16t + 4j + c in k-slot j, so the A
@@ -395,27 +396,33 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, j = lane >> 4, n = lane & 15;
-
-    // All pairs of a head on one XCD (blockIdx % 8): its K and dS blocks stay
-    // in that XCD's L2.
-    const int nbh_x = a.bh_pad / kXcds;
-    const int idx = blockIdx.x / kXcds;
-    const int pair = idx / nbh_x;
-    const int bh = blockIdx.x % kXcds + kXcds * (idx - pair * nbh_x);
-    if (bh >= a.B * a.H) return;
-    const int b = bh / a.H, h = bh - b * a.H;
+    const int it_end = a.sched.wg_start[blockIdx.x + 1];
+    int it = a.sched.wg_start[blockIdx.x];
+    if (it >= it_end) return;
     const int T = a.T, nqt = a.nqt;
-    const int jA = pair, jB = nqt - 1 - pair;  // jB == jA: the middle block of an odd nqt, alone
-    const int nA = jA + 1;
-    const int n_steps = nA + (jB != jA ? jB + 1 : 0);
 
-    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
-    const auto k_rows = head_rows(Kh, T, a.k.st);
+    // The step after (sit, skt) of block sj: the next tile of the block, or
+    // tile 0 of the next block of the list.  False at the end of the list.
+    auto advance = [&](int &sit, int &skt, int &sbh, int &sj) {
+        if (skt < sj) {
+            ++skt;
+            return true;
+        }
+        if (++sit >= it_end) return false;
+        const int item = a.sched.items[sit];
+        sbh = sched_bh(item);
+        sj = sched_j(item);
+        skt = 0;
+        return true;
+    };
+
     // Cooperative K tile load: thread (kg, c4) reads keys 4kg .. 4kg+3, dims
     // 4c4 .. 4c4+3 (rows past T read as zeros).
     const int kg = tid >> 4, c4 = tid & 15;
     f32x4 kpre[4];
-    auto prefetch_k = [&](int kt) {
+    auto prefetch_k = [&](int hbh, int kt) {
+        const int hb = hbh / a.H, hh = hbh - hb * a.H;
+        const auto k_rows = head_rows(a.k.p + hb * a.k.sb + hh * a.k.sh, T, a.k.st);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const uint32_t key = kt * kBwdBQ + 4 * kg + c;
@@ -425,17 +432,21 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
     // dS of the wave's 16 rows for tile kt of block jq: slice t (keys
     // 16t .. 16t+15) lies in block 2kt + t/2, columns 16(t%2) ...
     f32x4 dsn[4];
-    auto prefetch_ds = [&](int jq, int kt) {
+    auto prefetch_ds = [&](int hbh, int jq, int kt) {
         if (jq * kBwdBQ + 16 * w >= T) return;  // rows wholly past T: nothing to reduce
         const int nt = kt == jq ? w + 1 : 4;
-        const float *base = a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh, nqt, jq, 2 * kt)));
+        const float *base = a.ds + uniform(static_cast<uint32_t>(ds_block_offset(hbh, nqt, jq, 2 * kt)));
         const uint32_t off = (16 * w + n) * 32 + 4 * j;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
             if (t < nt) dsn[t] = *reinterpret_cast<const f32x4 *>(base + (t >> 1) * kDsBlock + off + 16 * (t & 1));
     };
-    prefetch_k(0);
-    prefetch_ds(jA, 0);
+
+    int kt = 0, bh = sched_bh(a.sched.items[it]), jq = sched_j(a.sched.items[it]);
+    prefetch_k(bh, 0);
+    prefetch_ds(bh, jq, 0);
+    int pit = it, pkt = 0, pbh = bh, pj = jq;  // the step whose loads are issued next
+    bool pre_ok = advance(pit, pkt, pbh, pj);
 
     f32x4 acc[4];  // acc[db][r] = dQ[q0 + 4j + r][4n + db] before the 1/sqrt(D) scaling
     f32x4 dsc[4];
@@ -451,10 +462,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
             }
     };
 
-    for (int s = 0; s < n_steps; ++s) {
-        const bool second = s >= nA;
-        const int jq = second ? jB : jA;     // query block
-        const int kt = second ? s - nA : s;  // key tile
+    for (;;) {
         const int q0 = jq * kBwdBQ + 16 * w;
         if (kt == 0) {
 #pragma unroll
@@ -470,36 +478,37 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) dsc[t] = dsn[t];
         __syncthreads();
-        if (s + 1 < n_steps) {
-            const bool nsecond = s + 1 >= nA;
-            const int nkt = nsecond ? s + 1 - nA : s + 1;
-            prefetch_k(nkt);
-            prefetch_ds(nsecond ? jB : jA, nkt);
+        if (pre_ok) {
+            prefetch_k(pbh, pkt);
+            prefetch_ds(pbh, pj, pkt);
+            pre_ok = advance(pit, pkt, pbh, pj);
         }
 
-        if (q0 >= T) continue;  // wave-uniform
-        const bool diag = kt == jq;
-        if (!diag) {
-            tile(IntC<4>{});
-            continue;
-        }
-        switch (w) {  // wave-uniform
-            case 0: tile(IntC<1>{}); break;
-            case 1: tile(IntC<2>{}); break;
-            case 2: tile(IntC<3>{}); break;
-            default: tile(IntC<4>{}); break;
-        }
-        // End of the block: dQ rows q0 + 4j + r.
-        float *dQh = a.dq.p + b * a.dq.sb + h * a.dq.sh + 4 * n;
+        if (q0 < T) {  // wave-uniform
+            if (kt != jq) {
+                tile(IntC<4>{});
+            } else {
+                switch (w) {  // wave-uniform
+                    case 0: tile(IntC<1>{}); break;
+                    case 1: tile(IntC<2>{}); break;
+                    case 2: tile(IntC<3>{}); break;
+                    default: tile(IntC<4>{}); break;
+                }
+                // End of the block: dQ rows q0 + 4j + r.
+                const int b = bh / a.H, h = bh - b * a.H;
+                float *dQh = a.dq.p + b * a.dq.sb + h * a.dq.sh + 4 * n;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int q = q0 + 4 * j + r;
-            if (q < T) {
-                const f32x4 val = {acc[0][r] * a.scale, acc[1][r] * a.scale, acc[2][r] * a.scale,
-                                   acc[3][r] * a.scale};
-                *reinterpret_cast<f32x4 *>(dQh + q * a.dq.st) = val;
+                for (int r = 0; r < 4; ++r) {
+                    const int q = q0 + 4 * j + r;
+                    if (q < T) {
+                        const f32x4 val = {acc[0][r] * a.scale, acc[1][r] * a.scale, acc[2][r] * a.scale,
+                                           acc[3][r] * a.scale};
+                        *reinterpret_cast<f32x4 *>(dQh + q * a.dq.st) = val;
+                    }
+                }
             }
         }
+        if (!advance(it, kt, bh, jq)) break;
     }
 }
 
@@ -539,8 +548,12 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
         hipCheck(hipEventRecord(ev[3], stream));
         hipCheck(hipEventRecord(ev[4], stream));
     }
-    if (p.full)
-        attn_bwd_dq16_kernel<<<dim3(((p.nqt + 1) / 2) * p.bh_pad), block, 0, stream>>>(p);
+    if (p.full) {
+        int num_wg = 0;
+        p.sched = device_block_schedule(p.B * p.H, p.nqt, reinterpret_cast<const void *>(attn_bwd_dq16_kernel),
+                                        stream, &num_wg);
+        attn_bwd_dq16_kernel<<<dim3(num_wg), block, 0, stream>>>(p);
+    }
     else if (p.vec)
         attn_bwd_dq_kernel<true, false><<<grid_q, block, 0, stream>>>(p);
     else

@@ -30,6 +30,7 @@ namespace gptc {
 constexpr int kFwdBM = 128;  // queries per workgroup
 constexpr int kFwdBN = 64;   // keys per LDS tile
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
+constexpr int kDeepMaxTiles = 2;      // heads of at most this many 64-key tiles: DEEP prefetch
 
 // FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the K/V tile loads
 // then go through bounds-checked buffer resources (no branches, no row tests).
@@ -239,13 +240,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     if (hf == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(l_tot)) * kLn2;
 }
 
-// ---- The 16-row forward (D == 64, buffer-resource loads): paired blocks ----
+// ---- The 16-row forward (D == 64, buffer-resource loads) ----
 //
-// One workgroup = 4 waves = one 64-query block j of one (b, h) and then the
-// block nqt-1-j of the same head.  A block j needs key tiles 0 .. j, so every
-// pair costs nqt + 1 tiles: all workgroups of the grid get the same work and
-// are resident together (with one block per workgroup the long blocks run
-// on, with their CUs half empty, after the short ones are done).
+// One workgroup = 4 waves runs the 64-query blocks of its work list
+// (block_sched.hpp) one after the other; block j of head bh reduces key
+// tiles 0 .. j.  The lists give every CU the same work (at B=8, H=12,
+// T=1024: blocks j and 15-j of one head per workgroup, all 768 workgroups
+// resident at once).  The key tiles of consecutive steps are prefetched
+// into registers one step ahead, across block and head boundaries.
 // Wave w owns queries 16w .. 16w+15 of the block; lane (g = lane/16,
 // i = lane%16) owns query i of them and, of every 16-key block, keys
 // 4g .. 4g+3 (the 16 x 16 x 4 accumulator layout of attn_common.hpp).  The
@@ -254,55 +256,78 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // Output row m of O^T block db is dim 4m + db, so that one 16-byte LDS read
 // of a V row gives a lane the A operands of all four blocks.  P' and m go
 // out in the same packed layout, so the backward is unchanged.
+//
+// DEEP (short sequences, where each workgroup runs one block of at most a
+// few tiles and latency dominates): tiles are prefetched two steps ahead,
+// so that a two-tile block issues all of its loads before its first wait.
 constexpr int kF16Rows = 64;  // queries per block of the 16-row kernel (4 waves x 16)
 
-template <bool PERM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_fwd16_kernel(const FwdParams a) {
+template <bool PERM, bool DEEP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEEP ? 2 : 3, DEEP ? 2 : 3))) void
+attn_fwd16_kernel(const FwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
     __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
-
-    // All pairs of a head on one XCD (blockIdx % 8), so its K and V stay in
-    // that XCD's L2.
-    const int nbh_x = a.bh_pad / kXcds;
-    const int idx = blockIdx.x / kXcds;
-    const int pair = idx / nbh_x;
-    const int bh = blockIdx.x % kXcds + kXcds * (idx - pair * nbh_x);
-    if (bh >= a.B * a.H) return;
-    const int b = bh / a.H, h = bh - b * a.H;
+    const int it_end = a.sched.wg_start[blockIdx.x + 1];
+    int it = a.sched.wg_start[blockIdx.x];
+    if (it >= it_end) return;
     const int T = a.T, nqt = a.nqt;
-    const int jA = pair, jB = nqt - 1 - pair;  // jB == jA: the middle block of an odd nqt, alone
-    const int nA = jA + 1;
-    const int n_steps = nA + (jB != jA ? jB + 1 : 0);
-
-    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
-    const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
-    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
-    const auto q_rows = head_rows(Qh, T, a.q.st);
-    const auto k_rows = head_rows(Kh, T, a.k.st);
-    const auto v_rows = head_rows(Vh, T, a.v.st);
 
     // Cooperative tile load: thread covers rows (tid>>4) + 16i, dims 4*(tid&15).
+    // Rows past T read as zeros (buffer resources over the head's T rows).
     const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
     f32x4 kpre[4], vpre[4];
-    auto prefetch = [&](int kt) {
+    f32x4 kpre2[4], vpre2[4];  // DEEP: the step after the prefetched one
+    auto load_tile = [&](int hbh, int kt, f32x4(&kd)[4], f32x4(&vd)[4]) {
+        const int hb = hbh / a.H, hh = hbh - hb * a.H;
+        const auto k_rows = head_rows(a.k.p + hb * a.k.sb + hh * a.k.sh, T, a.k.st);
+        const auto v_rows = head_rows(a.v.p + hb * a.v.sb + hh * a.v.sh, T, a.v.st);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t key = kt * kFwdBN + ld_row + 16 * i;
-            kpre[i] = buffer_load4(k_rows, key * a.k.st + ld_col);
-            vpre[i] = buffer_load4(v_rows, key * a.v.st + ld_col);
+            kd[i] = buffer_load4(k_rows, key * a.k.st + ld_col);
+            vd[i] = buffer_load4(v_rows, key * a.v.st + ld_col);
         }
     };
-    prefetch(0);
+    // The step after (sit, skt) of block sj: the next tile of the block, or
+    // tile 0 of the next block of the list.  False at the end of the list.
+    auto advance = [&](int &sit, int &skt, int &sbh, int &sj) {
+        if (skt < sj) {
+            ++skt;
+            return true;
+        }
+        if (++sit >= it_end) return false;
+        const int item = a.sched.items[sit];
+        sbh = sched_bh(item);
+        sj = sched_j(item);
+        skt = 0;
+        return true;
+    };
 
+    // Current step (it, kt) of block jq of head bh.
+    int kt = 0, bh = sched_bh(a.sched.items[it]), jq = sched_j(a.sched.items[it]);
+    int b = bh / a.H, h = bh - b * a.H;
     const float c2 = a.scale_log2;
     f32x4 qr[4];  // Q[my_q][16g + 4c + e] in qr[c][e]: the B operand of step 4c + e
+    auto load_q = [&]() {
+        const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
+        const int q = jq * kF16Rows + 16 * w + i16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c);
+    };
+    load_q();
+    load_tile(bh, 0, kpre, vpre);
+    // Prefetch cursor: the step whose tile sits in kpre2 (DEEP) or is loaded next.
+    int pit = it, pkt = 0, pbh = bh, pj = jq;
+    bool pre_ok = advance(pit, pkt, pbh, pj);
+    if (DEEP && pre_ok) load_tile(pbh, pkt, kpre2, vpre2);
+
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4 acc[4];  // O^T: acc[db][r] = O[my_q][16g + 4r + db] before the 1/l scaling
-    int jq = jA, kt = 0, my_q = 0;
+    int my_q = 0;
 
     // One key tile for this wave: NKB 16-key blocks of it are visible to the
     // wave's queries (DIAG: the tile holding the block's own keys, where block
@@ -383,16 +408,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             }
     };
 
-    for (int s = 0; s < n_steps; ++s) {
-        const bool second = s >= nA;
-        jq = second ? jB : jA;     // query block
-        kt = second ? s - nA : s;  // key tile
+    for (;;) {
         my_q = jq * kF16Rows + 16 * w + i16;
         if (kt == 0) {
-            // A new block: its Q rows (rows past T read as zeros) and fresh statistics.
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(my_q) * a.q.st + 16 * g + 4 * c);
+            // A new block: fresh statistics (its Q rows are loaded already
+            // for the first block, here for the others).
+            if (it != a.sched.wg_start[blockIdx.x]) load_q();
             if (PERM && my_q < T) {
                 float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * kDPad + 16 * g;
 #pragma unroll
@@ -424,33 +445,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             }
         }
         __syncthreads();
-        if (s + 1 < n_steps) prefetch(s + 1 < nA ? s + 1 : s + 1 - nA);
+        // Refill the prefetch registers: the next step's tile (DEEP: move it
+        // up and load the one after).
+        if (DEEP) {
+            if (pre_ok) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kpre[i] = kpre2[i];
+                    vpre[i] = vpre2[i];
+                }
+                pre_ok = advance(pit, pkt, pbh, pj);
+                if (pre_ok) load_tile(pbh, pkt, kpre2, vpre2);
+            }
+        } else if (pre_ok) {
+            load_tile(pbh, pkt, kpre, vpre);
+            pre_ok = advance(pit, pkt, pbh, pj);
+        }
 
         if (!diag) {
             tile(IntC<4>{}, std::false_type{});
-            continue;
-        }
-        switch (w) {  // wave-uniform
-            case 0: tile(IntC<1>{}, std::true_type{}); break;
-            case 1: tile(IntC<2>{}, std::true_type{}); break;
-            case 2: tile(IntC<3>{}, std::true_type{}); break;
-            default: tile(IntC<4>{}, std::true_type{}); break;
-        }
-
-        // End of the block: y = O / l and the log-sum-exp.
-        const float lt = sum4_rows(l_run);
-        if (my_q < T) {
-            const float inv = 1.0f / lt;
-            float *orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g;
-            float *o2row = a.o2 ? a.o2 + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g : nullptr;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const f32x4 val = {acc[0][r] * inv, acc[1][r] * inv, acc[2][r] * inv, acc[3][r] * inv};
-                *reinterpret_cast<f32x4 *>(orow + 4 * r) = val;
-                if (o2row) *reinterpret_cast<f32x4 *>(o2row + 4 * r) = val;
+        } else {
+            switch (w) {  // wave-uniform
+                case 0: tile(IntC<1>{}, std::true_type{}); break;
+                case 1: tile(IntC<2>{}, std::true_type{}); break;
+                case 2: tile(IntC<3>{}, std::true_type{}); break;
+                default: tile(IntC<4>{}, std::true_type{}); break;
             }
-            if (g == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(lt)) * kLn2;
+            // End of the block: y = O / l and the log-sum-exp.
+            const float lt = sum4_rows(l_run);
+            if (my_q < T) {
+                const float inv = 1.0f / lt;
+                float *orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g;
+                float *o2row = a.o2 ? a.o2 + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g : nullptr;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const f32x4 val = {acc[0][r] * inv, acc[1][r] * inv, acc[2][r] * inv, acc[3][r] * inv};
+                    *reinterpret_cast<f32x4 *>(orow + 4 * r) = val;
+                    if (o2row) *reinterpret_cast<f32x4 *>(o2row + 4 * r) = val;
+                }
+                if (g == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(lt)) * kLn2;
+            }
         }
+        if (!advance(it, kt, bh, jq)) break;
+        b = bh / a.H;
+        h = bh - b * a.H;
     }
 }
 
@@ -458,12 +496,24 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
     FwdParams p = p_in;
     const bool perm = p.qp != nullptr;
     if (p.full) {
-        const dim3 grid(((p.nqt + 1) / 2) * p.bh_pad), block(256);
+        // Short heads (at most kDeepMaxTiles key tiles) take the DEEP variant.
+        const bool deep = p.nqt <= kDeepMaxTiles;
+        const void *kern = deep ? (perm ? reinterpret_cast<const void *>(attn_fwd16_kernel<true, true>)
+                                        : reinterpret_cast<const void *>(attn_fwd16_kernel<false, true>))
+                                : (perm ? reinterpret_cast<const void *>(attn_fwd16_kernel<true, false>)
+                                        : reinterpret_cast<const void *>(attn_fwd16_kernel<false, false>));
+        int num_wg = 0;
+        p.sched = device_block_schedule(p.B * p.H, p.nqt, kern, stream, &num_wg);
+        const dim3 grid(num_wg), block(256);
         if (ev) hipCheck(hipEventRecord(ev[0], stream));
-        if (perm)
-            attn_fwd16_kernel<true><<<grid, block, 0, stream>>>(p);
+        if (deep && perm)
+            attn_fwd16_kernel<true, true><<<grid, block, 0, stream>>>(p);
+        else if (deep)
+            attn_fwd16_kernel<false, true><<<grid, block, 0, stream>>>(p);
+        else if (perm)
+            attn_fwd16_kernel<true, false><<<grid, block, 0, stream>>>(p);
         else
-            attn_fwd16_kernel<false><<<grid, block, 0, stream>>>(p);
+            attn_fwd16_kernel<false, false><<<grid, block, 0, stream>>>(p);
         hipCheck(hipGetLastError());
         if (ev) hipCheck(hipEventRecord(ev[1], stream));
         return;

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <cstddef>
 #include "attn_common.hpp"
+#include "block_sched.hpp"
 #include "grid_order.hpp"
 
 namespace gptc {
@@ -42,7 +43,8 @@ struct FwdParams {
     int bh_pad;           // B*H rounded up to a multiple of 8
     bool vec;             // D % 4 == 0 and every row 16-byte aligned
     bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
-    GridOrder order;      // grid order (set by launch_attn_fwd)
+    GridOrder order;      // grid order of the 32-row kernel (set by launch_attn_fwd)
+    BlockSched sched;     // work lists of the 16-row kernel (set by launch_attn_fwd)
 };
 
 struct BwdParams {
@@ -62,7 +64,8 @@ struct BwdParams {
     int bh_pad;
     bool vec;
     bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
-    GridOrder dq_order;   // grid order of the dq kernel (set by launch_attn_bwd)
+    GridOrder dq_order;   // grid order of the 32-row dq kernel (set by launch_attn_bwd)
+    BlockSched sched;     // work lists of the 16-row dq kernel (set by launch_attn_bwd)
 };
 
 // One KV-cache decode step (attn_decode.hip).

@@ -1,0 +1,177 @@
+// Host construction and device upload of the query-block work lists
+// (block_sched.hpp).
+#include "block_sched.hpp"
+
+#include <algorithm>
+#include <array>
+#include <map>
+#include <mutex>
+#include <numeric>
+#include <tuple>
+
+#include "gpu_kernels.h"
+#include "hip_check.hpp"
+#include "utils.h"
+
+namespace gptc {
+
+namespace {
+
+constexpr double kBlockOverhead = 0.5;  // Q load and epilogue of a block, in tiles
+
+double block_cost(int j) { return j + 1 + kBlockOverhead; }
+
+int pack(int bh, int j) { return (bh << kSchedJBits) | j; }
+
+// Largest per-CU sum of block costs of a table under the dispatch order.
+double max_cu_load(const SchedTable &t, int cus) {
+    std::vector<double> load(static_cast<size_t>(kSchedXcds) * cus, 0.0);
+    for (int w = 0; w < t.num_wg; ++w) {
+        const int x = w % kSchedXcds, u = (w / kSchedXcds) % cus;
+        for (int k = t.wg_start[w]; k < t.wg_start[w + 1]; ++k)
+            load[static_cast<size_t>(x) * cus + u] += block_cost(t.items[k] & ((1 << kSchedJBits) - 1));
+    }
+    return *std::max_element(load.begin(), load.end());
+}
+
+// Workgroup = blocks j and nqt-1-j of one head; heads fastest, so the pairs
+// of a head land on one XCD (blockIdx % 8 == bh % 8).
+SchedTable pairs_schedule(int BH, int nqt) {
+    SchedTable t;
+    const int bh_pad = (BH + kSchedXcds - 1) / kSchedXcds * kSchedXcds, nbh_x = bh_pad / kSchedXcds;
+    const int npair = (nqt + 1) / 2;
+    t.num_wg = npair * bh_pad;
+    t.wg_start.push_back(0);
+    for (int w = 0; w < t.num_wg; ++w) {
+        const int x = w % kSchedXcds, i = w / kSchedXcds;
+        const int pair = i / nbh_x, bh = x + kSchedXcds * (i - pair * nbh_x);
+        if (bh < BH) {
+            t.items.push_back(pack(bh, pair));
+            if (nqt - 1 - pair != pair) t.items.push_back(pack(bh, nqt - 1 - pair));
+        }
+        t.wg_start.push_back(static_cast<int>(t.items.size()));
+    }
+    t.pairs = true;
+    return t;
+}
+
+SchedTable lpt_schedule(int BH, int nqt, int per_cu, int cus) {
+    struct Item {
+        double cost;
+        int bh, j;
+    };
+    double per_head = 0.0;
+    for (int j = 0; j < nqt; ++j) per_head += block_cost(j);
+    const double target = per_head * BH / kSchedXcds;
+    // Heads dealt to XCDs in contiguous ranges of equal work (block granularity).
+    std::vector<std::vector<Item>> xitems(kSchedXcds);
+    double acc = 0.0;
+    for (int bh = 0; bh < BH; ++bh)
+        for (int j = 0; j < nqt; ++j) {
+            const double c = block_cost(j);
+            const int x = std::min(static_cast<int>((acc + 0.5 * c) / target), kSchedXcds - 1);
+            xitems[x].push_back({c, bh, j});
+            acc += c;
+        }
+    // slots[x][u][s]: the block list of slot s of CU u on XCD x.
+    std::vector<std::vector<std::vector<std::vector<int>>>> slots(
+        kSchedXcds, std::vector<std::vector<std::vector<int>>>(cus, std::vector<std::vector<int>>(per_cu)));
+    int rounds = 1;
+    for (int x = 0; x < kSchedXcds; ++x) {
+        auto &its = xitems[x];
+        std::stable_sort(its.begin(), its.end(), [](const Item &a, const Item &b) { return a.cost > b.cost; });
+        std::vector<double> cu(cus, 0.0);
+        std::vector<std::vector<double>> sl(cus, std::vector<double>(per_cu, 0.0));
+        for (const Item &it : its) {
+            const int u = static_cast<int>(std::min_element(cu.begin(), cu.end()) - cu.begin());
+            const int s = static_cast<int>(std::min_element(sl[u].begin(), sl[u].end()) - sl[u].begin());
+            cu[u] += it.cost;
+            sl[u][s] += it.cost;
+            slots[x][u][s].push_back(pack(it.bh, it.j));
+            rounds = std::max(rounds, s + 1);
+        }
+    }
+    SchedTable t;
+    t.num_wg = kSchedXcds * cus * rounds;
+    t.wg_start.push_back(0);
+    for (int w = 0; w < t.num_wg; ++w) {
+        const int x = w % kSchedXcds, i = w / kSchedXcds, u = i % cus, s = i / cus;
+        for (int item : slots[x][u][s]) t.items.push_back(item);
+        t.wg_start.push_back(static_cast<int>(t.items.size()));
+    }
+    return t;
+}
+
+struct DeviceTable {
+    int num_wg = 0;
+    int *wg_start = nullptr;
+    int *items = nullptr;
+    SchedTable host;  // kept: the source of the stream-ordered upload
+};
+
+std::mutex g_mu;
+std::map<std::tuple<int, int, int, int>, DeviceTable> g_tables;  // (device, BH, nqt, per_cu)
+std::map<std::pair<int, const void *>, std::pair<int, int>> g_occupancy;  // (device, kernel) -> (per_cu, cus)
+
+}  // namespace
+
+SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus) {
+    CHECK_ERROR(BH < 0 || nqt < 1 || nqt > (1 << kSchedJBits) || per_cu < 1 || cus < 1 ||
+                    static_cast<long long>(BH) >= (1LL << (31 - kSchedJBits)),
+                "block schedule: unsupported shape (heads %d, blocks %d, per CU %d, CUs %d).", BH, nqt, per_cu, cus);
+    SchedTable best = pairs_schedule(BH, nqt);
+    best.max_cu_load = max_cu_load(best, cus);
+    SchedTable lpt = lpt_schedule(BH, nqt, per_cu, cus);
+    lpt.max_cu_load = max_cu_load(lpt, cus);
+    // Pairs on ties: equal cost per workgroup also balances the workgroups of a CU.
+    if (lpt.max_cu_load < best.max_cu_load - 1e-9) best = std::move(lpt);
+    return best;
+}
+
+BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg) {
+    int dev = 0;
+    hipCheck(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_mu);
+    auto occ = g_occupancy.find({dev, kernel});
+    if (occ == g_occupancy.end()) {
+        int per_cu = 0, cus_total = 0;
+        hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0));
+        hipCheck(hipDeviceGetAttribute(&cus_total, hipDeviceAttributeMultiprocessorCount, dev));
+        const int cus = std::max(1, cus_total / kSchedXcds);
+        occ = g_occupancy.emplace(std::make_pair(dev, kernel), std::make_pair(std::max(1, per_cu), cus)).first;
+    }
+    const int per_cu = occ->second.first, cus = occ->second.second;
+    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus);
+    auto it = g_tables.find(key);
+    if (it == g_tables.end()) {
+        DeviceTable d;
+        d.host = build_block_schedule(BH, nqt, per_cu, cus);
+        d.num_wg = d.host.num_wg;
+        const size_t nw = d.host.wg_start.size() * sizeof(int), ni = std::max<size_t>(1, d.host.items.size()) * sizeof(int);
+        hipCheck(hipMalloc(&d.wg_start, nw));
+        hipCheck(hipMalloc(&d.items, ni));
+        hipCheck(hipMemcpyAsync(d.wg_start, d.host.wg_start.data(), nw, hipMemcpyHostToDevice, stream));
+        if (!d.host.items.empty())
+            hipCheck(hipMemcpyAsync(d.items, d.host.items.data(), d.host.items.size() * sizeof(int),
+                                    hipMemcpyHostToDevice, stream));
+        it = g_tables.emplace(key, std::move(d)).first;
+    }
+    *num_wg = it->second.num_wg;
+    return BlockSched{it->second.wg_start, it->second.items};
+}
+
+}  // namespace gptc
+
+// Host-side view of a table, for tests: fills wg_start (num_wg + 1 ints)
+// and items (cap ints) and returns num_wg (-1 if cap is too small).
+// per_cu and cus describe the GPU the table is built for.
+extern "C" int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items,
+                                             int cap, double *max_cu_load, int *used_pairs) {
+    const gptc::SchedTable t = gptc::build_block_schedule(BH, nqt, per_cu, cus);
+    if (static_cast<int>(t.items.size()) > cap || t.num_wg + 1 > cap) return -1;
+    std::copy(t.wg_start.begin(), t.wg_start.end(), wg_start);
+    std::copy(t.items.begin(), t.items.end(), items);
+    if (max_cu_load) *max_cu_load = t.max_cu_load;
+    if (used_pairs) *used_pairs = t.pairs ? 1 : 0;
+    return t.num_wg;
+}

@@ -240,6 +240,16 @@ long long gptc_decode_noalloc_scratch_floats(void);
  * gptc_attention_state_floats(B, T, C, n_heads): floats of the 1-D cache[3]
  * that the compact layout's forward expects (and otherwise re-points), so
  * that a layer can allocate it once at the right size.
+ *
+ * gptc_attention_block_schedule(BH, nqt, per_cu, cus, wg_start, items, cap,
+ *                               max_cu_load, used_pairs)
+ *   The work lists the D = 64 forward and dq kernels run for BH heads of nqt
+ *   64-query blocks on a GPU of 8 XCDs x cus CUs keeping per_cu workgroups
+ *   per CU (host computation only, for tests and tuning): workgroup w runs
+ *   the blocks items[wg_start[w] .. wg_start[w+1]), each (bh << 12) | j.
+ *   Returns the workgroup count (-1 when cap ints do not hold the table);
+ *   max_cu_load receives the largest per-CU sum of block costs (j + 1.5
+ *   tiles each), used_pairs 1 when the pairs construction was chosen.
  */
 /*
  * ---- one-token model step (KV-cache generation): no counterpart in gpt.c ----
@@ -261,6 +271,8 @@ void gptc_argmax_cuda(const tensor_t *logits, tensor_t *ids);
 void *gptc_stream(void);
 void gptc_set_kernel_events(void **events, int n);
 long long gptc_attention_state_floats(int B, int T, int C, int n_heads);
+int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
+                                  double *max_cu_load, int *used_pairs);
 
 #ifdef __cplusplus
 }

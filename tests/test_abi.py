@@ -139,3 +139,43 @@ def test_fatal_error_decode_position_past_cache():
     """)
     assert r.returncode == 1 and "survived" not in r.stdout
     assert "0 <= pos < L = 4" in r.stderr
+
+
+def block_schedule(lib, BH, nqt, per_cu=3, cus=32):
+    cap = BH * nqt + 8 * cus * per_cu * 4 + 16
+    ws, it = (ctypes.c_int * cap)(), (ctypes.c_int * cap)()
+    load, pairs = ctypes.c_double(), ctypes.c_int()
+    n = lib.gptc_attention_block_schedule(BH, nqt, per_cu, cus, ws, it, cap, ctypes.byref(load), ctypes.byref(pairs))
+    assert n > 0
+    starts = list(ws[:n + 1])
+    items = list(it[:starts[-1]])
+    return n, starts, items, load.value, bool(pairs.value)
+
+
+@pytest.mark.parametrize("B,H,T", [(8, 12, 1024), (4, 25, 1024), (8, 12, 128), (8, 12, 256), (1, 12, 1024),
+                                   (8, 12, 960), (2, 3, 17), (1, 1, 1), (3, 7, 2000), (16, 25, 1024)])
+def test_block_schedule_covers_every_block_once(lib, B, H, T):
+    """The forward and dq kernels write the rows of exactly the blocks their
+    work lists name: every (head, 64-query block) must appear exactly once,
+    or rows of y / dq would be left unwritten or written twice."""
+    BH, nqt = B * H, (T + 63) // 64
+    n, starts, items, load, pairs = block_schedule(lib, BH, nqt)
+    assert n % 8 == 0 and starts[0] == 0 and all(a <= b for a, b in zip(starts, starts[1:]))
+    seen = sorted((i >> 12, i & 4095) for i in items)
+    assert seen == [(bh, j) for bh in range(BH) for j in range(nqt)]
+    # The largest per-CU load is at least the even share and, for the paired
+    # shape of C2, exactly one CU's three pairs.
+    per_cu_share = BH * sum(j + 1.5 for j in range(nqt)) / (8 * 32)
+    assert load >= per_cu_share - 1e-9
+    if (B, H, T) == (8, 12, 1024):
+        assert pairs and abs(load - 3 * (nqt + 1 + 1.0)) < 1e-9
+
+
+def test_block_schedule_balances_c5(lib):
+    """C5 (100 heads x 16 blocks) has 800 pairs for 768 resident slots: the
+    longest-first lists must keep every CU within 5 % of the even share."""
+    BH, nqt = 4 * 25, 16
+    n, starts, items, load, pairs = block_schedule(lib, BH, nqt)
+    share = BH * sum(j + 1.5 for j in range(nqt)) / (8 * 32)
+    assert not pairs and n <= 8 * 32 * 3
+    assert load <= 1.05 * share, (load, share)
