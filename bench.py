@@ -509,8 +509,10 @@ def attention_bench(args):
     n_state = lib.gptc_attention_state_floats(B, T, C, H)
 
     def make_set(xin):
-        return (gptc.TensorP * 4)(xin, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((n_state,))), \
-            rt.empty((B, T, C))
+        # As Attention() sets it up: cache[1] is the output tensor itself
+        # (the layer keeps y for the backward by sharing its storage).
+        y = rt.empty((B, T, C))
+        return (gptc.TensorP * 4)(xin, y, rt.empty((B, H, T)), rt.empty((n_state,))), y
 
     caches, yt = make_set(xt)
     dqkv = rt.empty((B, T, 3 * C))
@@ -606,7 +608,7 @@ def attention_bench(args):
     # (rotating over enough input sets that every forward's inputs were
     # evicted by the others' traffic).
     ms_fwd_warm = timed(lambda i: fwd(), args.steps)
-    set_bytes = 4 * (B * T * 3 * C + 2 * B * T * C + B * H * T + n_state)
+    set_bytes = 4 * (B * T * 3 * C + B * T * C + B * H * T + n_state)
     n_sets = max(3, int(np.ceil(2 * 256e6 / set_bytes)) + 1)
     cold = [make_set(rt.from_numpy(x)) for _ in range(n_sets)] if n_sets * set_bytes < 8e9 else []
     ms_fwd_cold = None
@@ -617,8 +619,25 @@ def attention_bench(args):
         ms_fwd_cold = timed(lambda i: fwd(*cold[i % n_sets]), max(args.steps, 2 * n_sets))
         rt.sync()
         for c, y in cold:
-            for t in (*c, y):
+            for t in (c[0], c[2], c[3], y):
                 rt.free(t)
+    # The floor for moving the forward's compulsory bytes: a plain device
+    # copy of fwd_bytes / 2 (it reads and writes that much), timed cold the
+    # same way (forward-only configs).
+    copy_floor_us = None
+    if fwd_only:
+        n_copy = int(compulsory_bytes(B, T, C, H)[0] // 8)
+        n_cs = int(np.ceil(2 * 256e6 / (8 * n_copy))) + 1
+        srcs = [rt.from_numpy(np.ones(n_copy, np.float32)) for _ in range(n_cs)]
+        dsts = [rt.empty((n_copy,)) for _ in range(n_cs)]
+        for i in range(n_cs):
+            lib.tensor_copy(dsts[i], srcs[i])
+        rt.sync()
+        copy_floor_us = 1e3 * timed(lambda i: lib.tensor_copy(dsts[i % n_cs], srcs[i % n_cs]),
+                                    max(args.steps, 2 * n_cs))
+        rt.sync()
+        for t in srcs + dsts:
+            rt.free(t)
     step()  # leave the headline buffers with one fwd+bwd of the seeded inputs
     rt.sync()
 
@@ -665,6 +684,7 @@ def attention_bench(args):
             "gb_per_s_warm": round(fwd_bytes / (ms_fwd_warm * 1e-3) / 1e9, 1),
             "gb_per_s_cold": fwd_cold_gbs and round(fwd_cold_gbs, 1),
             "tflops_warm": round(2 * unit / (ms_fwd_warm * 1e-3) / 1e12, 3),
+            "copy_floor_us_cold": copy_floor_us and round(copy_floor_us, 3),
         },
         "api_ms": {"forward_median": round(statistics.median(api_f), 5),
                    "backward_median": round(statistics.median(api_b), 5),
@@ -718,7 +738,7 @@ def attention_bench(args):
     if not args.no_cpu_baseline:
         gpu_out = {"y": rt.to_numpy(yt), "lse": rt.to_numpy(caches[2]).reshape(B, H, T),
                    "dqkv": None if fwd_only else rt.to_numpy(dqkv)}
-    for t in (dyt, mask, yt, dqkv, *caches):
+    for t in (dyt, mask, yt, dqkv, caches[0], caches[2], caches[3]):
         rt.free(t)
     rt.sync()
 

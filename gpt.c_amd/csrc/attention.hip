@@ -170,14 +170,15 @@ extern "C" void attention_forward_cuda_kernel(const tensor_t *input, const tenso
     const bool compact = cache[0] == input || cache[0]->t == input->t;
     const StateLayout st = state_layout(d, !compact);
     if (compact) {
-        // Compact layout: the layer keeps the input itself, a copy of y in
-        // cache[1], the log-sum-exp in cache[2] and the backward state in
-        // cache[3] (re-pointed here unless it already has the state's size).
-        CHECK_ERROR(cache[1]->length != output->length, "Expected cache[1] of %d elements (copy of the output).",
+        // Compact layout: the layer keeps the input itself, y in cache[1]
+        // (the output's own storage, or a buffer that receives a copy), the
+        // log-sum-exp in cache[2] and the backward state in cache[3]
+        // (re-pointed here unless it already has the state's size).
+        CHECK_ERROR(cache[1]->length != output->length, "Expected cache[1] of %d elements (the output or a copy).",
                     output->length);
         CHECK_ERROR(cache[2]->length < bht, "Expected cache[2] of at least B*H*T = %lld elements.", (long long)bht);
         ensure_state_tensor(cache[3], st.total);
-        p.o2 = cache[1]->t;
+        p.o2 = cache[1]->t == output->t ? nullptr : cache[1]->t;
         p.lse = cache[2]->t;
         p.qp = p.kp = p.vp = nullptr;
     } else {

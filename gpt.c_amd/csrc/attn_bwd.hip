@@ -65,14 +65,20 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) 
 // ---- dK, dV (and the dS tiles) ----
 // FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the tile loads then
 // go through bounds-checked buffer resources (no branches, no row tests).
-template <bool VEC, bool FULL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_kernel(
-    const BwdParams a) {
+// RECOMP (short heads, whose forward stored no P'): P is recomputed as
+// exp2(S log2(e)/sqrt(D) - LSE log2(e)) with S = Q K^T formed like dP (Q rows
+// from LDS as A operands, this lane's K row in registers as B operands) and
+// the causal mask applied per element; one workgroup per head at T <= 128,
+// so the kernel may use the registers of one wave per SIMD.
+template <bool VEC, bool FULL, bool RECOMP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RECOMP ? 1 : 2, RECOMP ? 1 : 2))) void
+attn_bwd_dkdv_kernel(const BwdParams a) {
     __shared__ __attribute__((aligned(16))) float q_lds[kBwdBQ * kLdsStride];
     __shared__ __attribute__((aligned(16))) float do_lds[kBwdBQ * kLdsStride];
     // Per-query statistics of the tile, one entry per thread: [0, 128) the
     // factors f of P = P' * f for the workgroup's two 64-key tiles
-    // ([key tile][query]), [128, 192) delta, [192, 256) unused.
+    // ([key tile][query]; RECOMP: [0, 64) LSE log2(e), +inf past T),
+    // [128, 192) delta, [192, 256) unused.
     __shared__ __attribute__((aligned(16))) float stat_lds[256];
     const float *dl_lds = stat_lds + 2 * kBwdBQ;
 
@@ -104,6 +110,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f32x4 vr[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) vr[j] = k_ok ? load4<VEC>(Vh + my_k * a.v.st, 8 * j + 4 * hf, D) : zero4();
+    // RECOMP: the K row of this lane's key, dims 8j + 4hf + c: B operand of S = Q K^T.
+    f32x4 kr[RECOMP ? 8 : 1];
+    if (RECOMP) {
+        const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kr[j] = k_ok ? load4<VEC>(Kh + my_k * a.k.st, 8 * j + 4 * hf, D) : zero4();
+    }
     // Let these loads land here: a loop-invariant register with a load still
     // counted as outstanding makes every use in the loop wait for all loads.
     __builtin_amdgcn_s_waitcnt(0);
@@ -138,7 +151,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bool is_m = tid < 2 * kBwdBQ;
         const int kt = 2 * kb_idx + ((tid >> 6) & 1);
         st_ok = q < T && (!is_m || kt < n_qt);
-        st0 = *(is_m ? pm_h + min(kt, n_qt - 1) * T + qc : dl_h + qc);
+        st0 = RECOMP ? dl_h[qc] : *(is_m ? pm_h + min(kt, n_qt - 1) * T + qc : dl_h + qc);
         st1 = lse_h[qc];
     };
     if (qt0 < n_qt) prefetch(qt0);
@@ -161,7 +174,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh, n_qt, qt, kw0 >> 5)) + 32 * qb * 32);
     };
     auto load_p = [&](int qt, int qb) {
-        if (!half_needed(qt, qb)) return;
+        if (RECOMP || !half_needed(qt, qb)) return;
         const float *hb = half_base(qt, qb);
 #pragma unroll
         for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
@@ -181,7 +194,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         // Unconditional, so that no exec-masked branch sits between the loads
         // and their uses (branches make the wait counts conservative).
-        {
+        if (RECOMP) {
+            stat_lds[tid] = tid < kBwdBQ ? (st_ok ? st1 * kLog2e : INFINITY) : (st_ok ? st0 : 0.0f);
+        } else {
             const float f = fast_exp2(st0 - st1 * kLog2e);
             stat_lds[tid] = st_ok ? (tid < 2 * kBwdBQ ? f : st0) : 0.0f;
         }
@@ -203,11 +218,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                     for (int c = 0; c < 4; ++c) dp = mfma32(da[c], vr[j][c], dp);
                 }
+                if (RECOMP) {
+                    // S (queries x keys) for this half, then P with the causal mask.
+                    s = zero16();
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x4 f4 = *reinterpret_cast<const f32x4 *>(&f_w[32 * qb + 8 * g + 4 * hf]);
+                    for (int j = 0; j < 8; ++j) {
+                        const f32x4 qa = *reinterpret_cast<const f32x4 *>(
+                            &q_lds[(32 * qb + l32) * kLdsStride + 8 * j + 4 * hf]);
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) s[4 * g + c] = pbuf[4 * g + c] * f4[c];  // P
+                        for (int c = 0; c < 4; ++c) s = mfma32(qa[c], kr[j][c], s);
+                    }
+                    const float c2 = a.scale * kLog2e;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&stat_lds[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const int q = qt * kBwdBQ + 32 * qb + 8 * g + 4 * hf + c;
+                            const float p = fast_exp2(fmaf(s[4 * g + c], c2, -l4[c]));
+                            s[4 * g + c] = my_k > q ? 0.0f : p;  // P
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 f4 = *reinterpret_cast<const f32x4 *>(&f_w[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) s[4 * g + c] = pbuf[4 * g + c] * f4[c];  // P
+                    }
                 }
             }
             // The next half's P' (its registers are free now).
@@ -537,12 +575,14 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
         hipCheck(hipEventRecord(ev[1], stream));
         hipCheck(hipEventRecord(ev[2], stream));
     }
-    if (p.full)
-        attn_bwd_dkdv_kernel<true, true><<<grid_k, block, 0, stream>>>(p);
+    if (p.full && p.nqt <= kShortHeadTiles)
+        attn_bwd_dkdv_kernel<true, true, true><<<grid_k, block, 0, stream>>>(p);
+    else if (p.full)
+        attn_bwd_dkdv_kernel<true, true, false><<<grid_k, block, 0, stream>>>(p);
     else if (p.vec)
-        attn_bwd_dkdv_kernel<true, false><<<grid_k, block, 0, stream>>>(p);
+        attn_bwd_dkdv_kernel<true, false, false><<<grid_k, block, 0, stream>>>(p);
     else
-        attn_bwd_dkdv_kernel<false, false><<<grid_k, block, 0, stream>>>(p);
+        attn_bwd_dkdv_kernel<false, false, false><<<grid_k, block, 0, stream>>>(p);
     hipCheck(hipGetLastError());
     if (ev) {
         hipCheck(hipEventRecord(ev[3], stream));

@@ -30,7 +30,6 @@ namespace gptc {
 constexpr int kFwdBM = 128;  // queries per workgroup
 constexpr int kFwdBN = 64;   // keys per LDS tile
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
-constexpr int kDeepMaxTiles = 2;      // heads of at most this many 64-key tiles: DEEP prefetch
 
 // FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the K/V tile loads
 // then go through bounds-checked buffer resources (no branches, no row tests).
@@ -385,8 +384,9 @@ attn_fwd16_kernel(const FwdParams a) {
         l_run += ls[0] + ls[1];
 
         // P' rows of block (jq, key blocks 2kt and 2kt + 1), zeros past the
-        // diagonal; m of this tile.
-        {
+        // diagonal; m of this tile (not for short heads, whose backward
+        // recomputes P: pp == nullptr).
+        if (a.pp != nullptr) {
             float *ptile = a.pp + ds_block_offset(bh, nqt, jq, 2 * kt);  // uniform
             const uint32_t prow = (16 * w + i16) * 32 + 4 * g;
 #pragma unroll
@@ -445,19 +445,10 @@ attn_fwd16_kernel(const FwdParams a) {
             }
         }
         __syncthreads();
-        // Refill the prefetch registers: the next step's tile (DEEP: move it
-        // up and load the one after).
-        if (DEEP) {
-            if (pre_ok) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    kpre[i] = kpre2[i];
-                    vpre[i] = vpre2[i];
-                }
-                pre_ok = advance(pit, pkt, pbh, pj);
-                if (pre_ok) load_tile(pbh, pkt, kpre2, vpre2);
-            }
-        } else if (pre_ok) {
+        // Refill the prefetch registers with the next step's tile.  DEEP: it
+        // is in flight already (kpre2); it moves up after this step's tile,
+        // so that this tile's compute does not wait for its loads.
+        if (!DEEP && pre_ok) {
             load_tile(pbh, pkt, kpre, vpre);
             pre_ok = advance(pit, pkt, pbh, pj);
         }
@@ -486,6 +477,15 @@ attn_fwd16_kernel(const FwdParams a) {
                 if (g == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(lt)) * kLn2;
             }
         }
+        if (DEEP && pre_ok) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kpre[i] = kpre2[i];
+                vpre[i] = vpre2[i];
+            }
+            pre_ok = advance(pit, pkt, pbh, pj);
+            if (pre_ok) load_tile(pbh, pkt, kpre2, vpre2);
+        }
         if (!advance(it, kt, bh, jq)) break;
         b = bh / a.H;
         h = bh - b * a.H;
@@ -496,8 +496,9 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
     FwdParams p = p_in;
     const bool perm = p.qp != nullptr;
     if (p.full) {
-        // Short heads (at most kDeepMaxTiles key tiles) take the DEEP variant.
-        const bool deep = p.nqt <= kDeepMaxTiles;
+        // Short heads take the DEEP variant and leave P' to the backward.
+        const bool deep = p.nqt <= kShortHeadTiles;
+        if (deep) p.pp = p.pm = nullptr;
         const void *kern = deep ? (perm ? reinterpret_cast<const void *>(attn_fwd16_kernel<true, true>)
                                         : reinterpret_cast<const void *>(attn_fwd16_kernel<false, true>))
                                 : (perm ? reinterpret_cast<const void *>(attn_fwd16_kernel<true, false>)

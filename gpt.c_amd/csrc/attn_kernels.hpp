@@ -25,6 +25,13 @@ __host__ __device__ inline size_t ds_block_offset(int bh, int nqt, int qt, int k
     return (static_cast<size_t>(bh) * nqt * (nqt + 1) + static_cast<size_t>(qt) * (qt + 1) + kb32) * kDsBlock;
 }
 
+// Short heads: at most this many 64-key tiles (T <= 128).  Their forward
+// (D = 64) is latency-bound: it prefetches two tiles ahead and does not
+// store P' or m; their dk/dv kernel recomputes P = exp2(S log2(e)/sqrt(D)
+// - LSE log2(e)) from Q, K and the saved LSE instead.  The dS blocks keep
+// their place in the state either way.
+constexpr int kShortHeadTiles = 2;
+
 // Floats of the packed P' / dS blocks for a (B, H, T) problem.
 size_t bwd_ds_floats(int B, int H, int T);
 

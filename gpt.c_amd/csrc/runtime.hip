@@ -13,6 +13,11 @@
 // no event or synchronisation.  Size classes: multiples of 512 B up to
 // 1 MiB, multiples of 2 MiB above.  When the device runs out of memory the
 // cache is returned to the device and the request retried once.
+//
+// Shared blocks.  gptc_retain_cuda() adds an owner to a live block: two
+// tensors can then hold one buffer (the attention layer keeps its output
+// for the backward that way instead of copying it), and the block returns
+// to the cache when the last owner frees it.
 #include <cstdint>
 #include <map>
 #include <mutex>
@@ -28,7 +33,11 @@ bool g_ready = false;
 bool g_pool_alloc = false;  // device supports stream-ordered allocation
 
 std::mutex g_alloc_mu;
-std::unordered_map<void *, size_t> g_live;  // block -> size class, in use
+struct LiveBlock {
+    size_t cls;  // size class
+    int refs;    // owners (1 + retains)
+};
+std::unordered_map<void *, LiveBlock> g_live;  // blocks in use
 std::multimap<size_t, void *> g_cached;     // size class -> free block
 size_t g_cached_bytes = 0;
 
@@ -124,8 +133,16 @@ extern "C" void *alloc_cuda(const size_t nbytes) {
         }
         hipCheck(err);
     }
-    g_live.emplace(ptr, cls);
+    g_live.emplace(ptr, LiveBlock{cls, 1});
     return ptr;
+}
+
+extern "C" void gptc_retain_cuda(void *ptr) {
+    REQUIRE_ARG(ptr);
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    auto it = g_live.find(ptr);
+    CHECK_ERROR(it == g_live.end(), "gptc_retain_cuda: %p is not a live block of alloc_cuda.", ptr);
+    ++it->second.refs;
 }
 
 extern "C" void free_cuda(void *ptr) {
@@ -137,7 +154,8 @@ extern "C" void free_cuda(void *ptr) {
         device_free(ptr);
         return;
     }
-    g_cached.emplace(it->second, ptr);
-    g_cached_bytes += it->second;
+    if (--it->second.refs > 0) return;  // another owner still holds the block
+    g_cached.emplace(it->second.cls, ptr);
+    g_cached_bytes += it->second.cls;
     g_live.erase(it);
 }

@@ -159,6 +159,7 @@ SIGNATURES = {
     "attention_decode_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
     "attention_decode_noalloc_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
     "gptc_decode_noalloc_scratch_floats": (ctypes.c_longlong, []),
+    "gptc_retain_cuda": (None, [_vp]),
     "gptc_attention_block_schedule": (_ci, [_ci, _ci, _ci, _ci, ctypes.POINTER(_ci), ctypes.POINTER(_ci), _ci,
                                              ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_ci)]),
     "saxpy_cuda": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),

@@ -26,6 +26,10 @@ void synchronize_cuda(void);
 /* ---- stream-ordered allocation: replaces kernels/src/cuda/Alloc.h:10-12 ---- */
 void *alloc_cuda(const size_t nbytes);
 void free_cuda(void *ptr);
+/* No counterpart in the reference: adds an owner to a block returned by
+ * alloc_cuda, so that it survives until free_cuda has been called once per
+ * owner (a tensor that shares another tensor's storage). */
+void gptc_retain_cuda(void *ptr);
 
 /* ---- tensor data ops: replace kernels/src/cuda/Tensor.h:9-17 ---- */
 void move_tensor_to_host_cuda(tensor_t *tensor);
@@ -49,7 +53,9 @@ void copy_tensor_data_cuda(tensor_t *dst, const tensor_t *src);
  *          accepted and told apart by cache[0]:
  *          - compact (this library's attention.c): cache[0] IS the input
  *            tensor (ownership passed to the layer), cache[1] (B, T, C)
- *            receives a copy of the output, cache[2] (B, H, T) receives the
+ *            is the output's storage itself (attention.c shares it) or,
+ *            when it is a buffer of its own, receives a copy of the
+ *            output; cache[2] (B, H, T) receives the
  *            row log-sum-exp, cache[3] receives the backward state: the
  *            causal blocks of the probabilities (about B*H*T*T/2 floats)
  *            and their per-tile row maxima.  A cache[3] that is not a 1-D
