@@ -75,9 +75,11 @@ int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 //   [y copy (B*T*C) | log-sum-exp (B*H*T)]   reference cache layout only
 //   delta (B*H*T)                            written by the backward
 //   m (B*H*nqt*T)                            per-tile row maxima of P'
+//   db partials (B*nqt*C + B*nkb*2C)        column sums of the dq | dk, dv
+//                                            rows (qkv bias folded in only)
 //   P' / dS blocks (bwd_ds_floats)           P' from forward, dS in backward
 struct StateLayout {
-    int64_t y, lse, delta, m, p, total;
+    int64_t y, lse, delta, m, dbq, dbkv, p, total;
 };
 
 StateLayout state_layout(const Dims &d, bool reference_layout) {
@@ -96,6 +98,11 @@ StateLayout state_layout(const Dims &d, bool reference_layout) {
     off += align64(bht);
     s.m = off;
     off += align64(bht * nqt);
+    const int64_t nkb = (d.T + 127) / 128;
+    s.dbq = off;
+    off += align64(static_cast<int64_t>(d.B) * nqt * d.C);
+    s.dbkv = off;
+    off += align64(static_cast<int64_t>(d.B) * nkb * 2 * d.C);
     s.p = off;
     off += static_cast<int64_t>(gptc::bwd_ds_floats(d.B, d.H, d.T));
     s.total = off;
@@ -137,8 +144,14 @@ extern "C" void gptc_set_kernel_events(void **events, int n) {
     g_have_events = true;
 }
 
-extern "C" void attention_forward_cuda_kernel(const tensor_t *input, const tensor_t *mask, const int n_heads,
-                                              tensor_t **cache, tensor_t *output) {
+namespace {
+
+// The forward of both entry points.  bias: the qkv Linear's bias (3C),
+// nullptr when the input already includes it.  With a bias, the compact
+// layout is required; the D = 64 kernels add it as they load q, k, v, other
+// head sizes get it added to the input in place first.
+void forward_impl(const tensor_t *input, const tensor_t *bias, const tensor_t *mask, const int n_heads,
+                  tensor_t **cache, tensor_t *output) {
     CHECK_ERROR(input == NULL || mask == NULL || output == NULL || cache == NULL,
                 "Expected input, mask, cache and output to be non-NULL.");
     for (int i = 0; i < 4; i++) CHECK_ERROR(cache[i] == NULL, "Expected cache[%d] to be allocated.", i);
@@ -209,11 +222,47 @@ extern "C" void attention_forward_cuda_kernel(const tensor_t *input, const tenso
     p.vec = (d.D % 4 == 0) && aligned16(input->t) && aligned16(output->t) && aligned16(p.o2) &&
             (!p.qp || (aligned16(p.qp) && aligned16(p.kp) && aligned16(p.vp)));
     p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.v.st});
+    if (bias != nullptr) {
+        CHECK_ERROR(!compact, "The qkv bias can be folded in with the compact cache layout only.");
+        CHECK_ERROR(bias->device != CUDA || bias->length != 3 * d.C, "Expected a GPU bias of 3C = %d elements.",
+                    3 * d.C);
+        const bool folded = p.full && aligned16(bias->t);
+        if (folded) {
+            p.qb = bias->t;
+            p.kb = bias->t + d.C;
+            p.vb = bias->t + 2 * d.C;
+        } else {
+            // The input is the layer's own (cache[0]): add the bias in place.
+            gptc::launch_bias_add(input->t, bias->t, static_cast<int64_t>(d.B) * d.T, 3 * d.C, gptc_stream_checked());
+        }
+        // The backward must know whether the input still lacks the bias: the
+        // state is 1-D, so its unused second shape entry records it.
+        cache[3]->shape[1] = folded ? 1 : 0;
+    } else if (compact) {
+        cache[3]->shape[1] = 0;
+    }
     gptc::launch_attn_fwd(p, gptc_stream_checked(), g_have_events ? g_events : nullptr);
 }
 
-extern "C" void attention_backward_cuda_kernel(const tensor_t *global_grad, tensor_t **cache, const int n_heads,
-                                               tensor_t *dout) {
+}  // namespace
+
+extern "C" void attention_forward_cuda_kernel(const tensor_t *input, const tensor_t *mask, const int n_heads,
+                                              tensor_t **cache, tensor_t *output) {
+    forward_impl(input, nullptr, mask, n_heads, cache, output);
+}
+
+extern "C" void gptc_attention_forward_qkv_bias(const tensor_t *input, const tensor_t *bias, const tensor_t *mask,
+                                                const int n_heads, tensor_t **cache, tensor_t *output) {
+    REQUIRE_ARG(bias);
+    forward_impl(input, bias, mask, n_heads, cache, output);
+}
+
+namespace {
+
+// The backward of both entry points: bias and db given (db += the column
+// sums of dout) when the forward took the bias.
+void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t *bias, const int n_heads,
+                   tensor_t *dout, tensor_t *db) {
     CHECK_ERROR(global_grad == NULL || cache == NULL || dout == NULL,
                 "Expected global_grad, cache and dout to be non-NULL.");
     for (int i = 0; i < 4; i++)
@@ -282,7 +331,54 @@ extern "C" void attention_backward_cuda_kernel(const tensor_t *global_grad, tens
     p.vec = (d.D % 4 == 0) && aligned16(p.q.p) && aligned16(p.k.p) && aligned16(p.v.p) && aligned16(y_saved) &&
             aligned16(global_grad->t) && aligned16(dout->t);
     p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.dout.st});
-    gptc::launch_attn_bwd(p, gptc_stream_checked(), g_have_events ? g_events + 2 : nullptr);
+    hipStream_t s = gptc_stream_checked();
+    bool folded = false;
+    if (bias != nullptr) {
+        CHECK_ERROR(!compact, "The qkv bias can be folded in with the compact cache layout only.");
+        CHECK_ERROR(db == NULL || db->device != CUDA || db->length != 3 * d.C || bias->length != 3 * d.C,
+                    "Expected a GPU bias and db of 3C = %d elements.", 3 * d.C);
+        // Whether the forward left the bias out of the input (recorded in the
+        // state's unused second shape entry).  If so and these kernels cannot
+        // fold it in (a differently aligned dy or dout), add it to the input.
+        const bool fwd_folded = cache[3]->shape[1] == 1;
+        folded = fwd_folded && p.full;
+        if (fwd_folded && !folded)
+            gptc::launch_bias_add(const_cast<float *>(c0->t), bias->t, static_cast<int64_t>(d.B) * d.T, 3 * d.C, s);
+        if (folded) {
+            p.qb = bias->t;
+            p.kb = bias->t + d.C;
+            p.vb = bias->t + 2 * d.C;
+            p.db = db->t;
+            p.dbq_part = cache[3]->t + st.dbq;
+            p.dbkv_part = cache[3]->t + st.dbkv;
+            p.C = d.C;
+        }
+    }
+    gptc::launch_attn_bwd(p, s, g_have_events ? g_events + 2 : nullptr);
+    if (bias != nullptr) {
+        const int nqt = (d.T + 63) / 64, nkb = (d.T + 127) / 128;
+        if (folded) {
+            // db += the per-block column sums, in a fixed order.
+            gptc::launch_add_column_partials(p.dbq_part, db->t, d.B * nqt, d.C, s);
+            gptc::launch_add_column_partials(p.dbkv_part, db->t + d.C, d.B * nkb, 2 * d.C, s);
+        } else {
+            gptc::launch_column_sum_add(dout->t, db->t, d.B * d.T, 3 * d.C, s);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" void attention_backward_cuda_kernel(const tensor_t *global_grad, tensor_t **cache, const int n_heads,
+                                               tensor_t *dout) {
+    backward_impl(global_grad, cache, nullptr, n_heads, dout, nullptr);
+}
+
+extern "C" void gptc_attention_backward_qkv_bias(const tensor_t *global_grad, tensor_t **cache, const tensor_t *bias,
+                                                 const int n_heads, tensor_t *dout, tensor_t *db) {
+    REQUIRE_ARG(bias);
+    REQUIRE_ARG(db);
+    backward_impl(global_grad, cache, bias, n_heads, dout, db);
 }
 
 extern "C" long long gptc_attention_state_floats(int B, int T, int C, int n_heads) {

@@ -81,6 +81,10 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     // [128, 192) delta, [192, 256) unused.
     __shared__ __attribute__((aligned(16))) float stat_lds[256];
     const float *dl_lds = stat_lds + 2 * kBwdBQ;
+    // The q bias of the head (FULL kernels with the qkv bias folded in),
+    // added to the Q tile as it is stored; then the db column sums.
+    __shared__ __attribute__((aligned(16))) float qb_lds[kDPad];
+    __shared__ float red_lds[4][2 * kDPad];
 
     const int tid = threadIdx.x;
     // The wave index is made visibly uniform (an SGPR): branches on it are then
@@ -117,9 +121,32 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) kr[j] = k_ok ? load4<VEC>(Kh + my_k * a.k.st, 8 * j + 4 * hf, D) : zero4();
     }
+    // The qkv bias (FULL only): added to this key's V (and K) row here, to
+    // the Q tiles through qb_lds.  Keys past T keep a zero row.
+    const bool biased = FULL && a.qb != nullptr;
+    f32x4 vbias[8], kbias[RECOMP ? 8 : 1];
+    f32x4 qb4 = zero4();
+    if (biased) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            vbias[j] = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 8 * j + 4 * hf);
+            if (RECOMP) kbias[j] = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + 8 * j + 4 * hf);
+        }
+        if (tid < kDPad / 4) qb4 = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 4 * tid);
+    }
     // Let these loads land here: a loop-invariant register with a load still
     // counted as outstanding makes every use in the loop wait for all loads.
     __builtin_amdgcn_s_waitcnt(0);
+    if (biased) {
+        if (k_ok) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                vr[j] += vbias[j];
+                if (RECOMP) kr[j] += kbias[j];
+            }
+        }
+        if (tid < kDPad / 4) *reinterpret_cast<f32x4 *>(&qb_lds[4 * tid]) = qb4;
+    }
 
     const int qt0 = k_blk0 / kBwdBQ;
     const int n_qt = a.nqt;
@@ -186,6 +213,13 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 
     for (int qt = qt0; qt < n_qt; ++qt) {
         __syncthreads();
+        if (biased) {
+            // Q rows past T hold the bias too: their dO rows are zero and
+            // their P is 0 (f = 0, or the +inf LSE of RECOMP), so they add nothing.
+            const f32x4 qb = *reinterpret_cast<const f32x4 *>(&qb_lds[ld_col]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qpre[i] += qb;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = ld_row + 16 * i;
@@ -304,6 +338,33 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
                 dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
                 dVh[key * a.dv.st + dim] = acc_dv[db][r];
             }
+        }
+    }
+    if (FULL && a.db != nullptr) {
+        // db of the k and v parts: column sums of this workgroup's 128 dK and
+        // dV rows (keys < T), in a fixed order: registers, lane halves, waves.
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+            float sk = 0.0f, sv = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const bool ok = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3) < T;
+                sk += ok ? acc_dk[db][r] : 0.0f;
+                sv += ok ? acc_dv[db][r] : 0.0f;
+            }
+            sk += other_half(sk);
+            sv += other_half(sv);
+            if (hf == 0) {
+                red_lds[w][32 * db + l32] = sk * a.scale;
+                red_lds[w][kDPad + 32 * db + l32] = sv;
+            }
+        }
+        __syncthreads();
+        if (tid < 2 * kDPad) {
+            const float s = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
+            // Row (b, key block) of the (B*nkb) x 2C partials: dk part, then dv part.
+            const int col = (tid < kDPad ? 0 : a.C) + h * kDPad + (tid & (kDPad - 1));
+            a.dbkv_part[(static_cast<size_t>(b) * a.nkb + kb_idx) * 2 * a.C + col] = s;
         }
     }
 }
@@ -430,6 +491,7 @@ constexpr int kDq16KStride = 256;  // floats per group of 4 keys in k_lds
 
 __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[16 * kDq16KStride];
+    __shared__ float red_lds[4][kDPad];  // db column sums of the block's dQ rows, per wave
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -457,7 +519,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
     // Cooperative K tile load: thread (kg, c4) reads keys 4kg .. 4kg+3, dims
     // 4c4 .. 4c4+3 (rows past T read as zeros).
     const int kg = tid >> 4, c4 = tid & 15;
+    const bool biased = a.kb != nullptr;  // the qkv bias is added to the K tile here
     f32x4 kpre[4];
+    f32x4 kbias = zero4();  // bias of dims 4c4 .. 4c4+3 for the head of the tile in kpre
     auto prefetch_k = [&](int hbh, int kt) {
         const int hb = hbh / a.H, hh = hbh - hb * a.H;
         const auto k_rows = head_rows(a.k.p + hb * a.k.sb + hh * a.k.sh, T, a.k.st);
@@ -466,6 +530,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
             const uint32_t key = kt * kBwdBQ + 4 * kg + c;
             kpre[c] = buffer_load4(k_rows, key * a.k.st + 4 * c4);
         }
+        if (biased) kbias = *reinterpret_cast<const f32x4 *>(a.kb + hh * kDPad + 4 * c4);
     };
     // dS of the wave's 16 rows for tile kt of block jq: slice t (keys
     // 16t .. 16t+15) lies in block 2kt + t/2, columns 16(t%2) ...
@@ -508,6 +573,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
         }
 
         __syncthreads();
+        if (biased) {
+            // K rows past T hold the bias too: the dS this kernel reads for
+            // them is zero (the dk/dv kernel writes zeros for keys past T in
+            // every 32-key block that holds a key below T).
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kpre[c] += kbias;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const f32x4 v = {kpre[0][e], kpre[1][e], kpre[2][e], kpre[3][e]};
@@ -544,6 +616,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
                         *reinterpret_cast<f32x4 *>(dQh + q * a.dq.st) = val;
                     }
                 }
+            }
+        }
+        if (a.db != nullptr && kt == jq) {
+            // db of the q part: column sums of the block's 64 dQ rows (rows
+            // < T) in a fixed order: registers, the 4 row groups j, waves.
+            // Every wave takes part (waves wholly past T add zeros).
+            f32x4 cs = zero4();
+            if (q0 < T) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (q0 + 4 * j + r < T) cs += f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                cs[e] += __shfl_xor(cs[e], 16, 64);
+                cs[e] += __shfl_xor(cs[e], 32, 64);
+            }
+            if (j == 0) *reinterpret_cast<f32x4 *>(&red_lds[w][4 * n]) = cs * a.scale;
+            __syncthreads();
+            if (tid < kDPad) {
+                const int b = bh / a.H, h = bh - b * a.H;
+                // red_lds[w][4n + e] holds dim 4n + e (acc[e] is dim 4n + e).
+                const float s = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
+                a.dbq_part[(static_cast<size_t>(b) * nqt + jq) * a.C + h * kDPad + tid] = s;
             }
         }
         if (!advance(it, kt, bh, jq)) break;

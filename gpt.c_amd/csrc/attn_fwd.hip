@@ -266,6 +266,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEEP ? 2 : 
 attn_fwd16_kernel(const FwdParams a) {
     __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
     __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
+    // The qkv bias of the current step's head (q | k | v, 64 floats each).
+    __shared__ __attribute__((aligned(16))) float bias_lds[3 * kDPad];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -278,9 +280,20 @@ attn_fwd16_kernel(const FwdParams a) {
     // Cooperative tile load: thread covers rows (tid>>4) + 16i, dims 4*(tid&15).
     // Rows past T read as zeros (buffer resources over the head's T rows).
     const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    // The qkv Linear's bias is added here (compact layout only: never with PERM).
+    const bool biased = !PERM && a.kb != nullptr;
     f32x4 kpre[4], vpre[4];
     f32x4 kpre2[4], vpre2[4];  // DEEP: the step after the prefetched one
-    auto load_tile = [&](int hbh, int kt, f32x4(&kd)[4], f32x4(&vd)[4]) {
+    // Threads 0..47 carry one float4 of the q | k | v bias of the head of the
+    // tile in kpre (bpre) and in kpre2 (bpre2, DEEP): loaded with the tile,
+    // written to bias_lds at the start of the step that stores the tile, and
+    // added there (K, V) and to the block's Q rows (qr) after the step's
+    // second barrier.
+    const bool bias_lane = biased && tid < 3 * kDPad / 4;
+    const float *bias_src = tid < kDPad / 4 ? a.qb : tid < kDPad / 2 ? a.kb : a.vb;
+    const int bias_dim = 4 * (tid & 15);
+    f32x4 bpre = zero4(), bpre2 = zero4();
+    auto load_tile = [&](int hbh, int kt, f32x4(&kd)[4], f32x4(&vd)[4], f32x4 &bd) {
         const int hb = hbh / a.H, hh = hbh - hb * a.H;
         const auto k_rows = head_rows(a.k.p + hb * a.k.sb + hh * a.k.sh, T, a.k.st);
         const auto v_rows = head_rows(a.v.p + hb * a.v.sb + hh * a.v.sh, T, a.v.st);
@@ -290,6 +303,7 @@ attn_fwd16_kernel(const FwdParams a) {
             kd[i] = buffer_load4(k_rows, key * a.k.st + ld_col);
             vd[i] = buffer_load4(v_rows, key * a.v.st + ld_col);
         }
+        if (bias_lane) bd = *reinterpret_cast<const f32x4 *>(bias_src + hh * kDPad + bias_dim);
     };
     // The step after (sit, skt) of block sj: the next tile of the block, or
     // tile 0 of the next block of the list.  False at the end of the list.
@@ -318,11 +332,11 @@ attn_fwd16_kernel(const FwdParams a) {
         for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c);
     };
     load_q();
-    load_tile(bh, 0, kpre, vpre);
+    load_tile(bh, 0, kpre, vpre, bpre);
     // Prefetch cursor: the step whose tile sits in kpre2 (DEEP) or is loaded next.
     int pit = it, pkt = 0, pbh = bh, pj = jq;
     bool pre_ok = advance(pit, pkt, pbh, pj);
-    if (DEEP && pre_ok) load_tile(pbh, pkt, kpre2, vpre2);
+    if (DEEP && pre_ok) load_tile(pbh, pkt, kpre2, vpre2, bpre2);
 
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4 acc[4];  // O^T: acc[db][r] = O[my_q][16g + 4r + db] before the 1/l scaling
@@ -425,7 +439,22 @@ attn_fwd16_kernel(const FwdParams a) {
             for (int db = 0; db < 4; ++db) acc[db] = zero4();
         }
 
+        // The bias of this step's head; the previous step's readers of
+        // bias_lds are past its second barrier.
+        if (bias_lane) *reinterpret_cast<f32x4 *>(&bias_lds[4 * tid]) = bpre;
         __syncthreads();
+        if (biased) {
+            // Rows past T read as zeros and then hold the bias: they only
+            // occur in a block's diagonal tile, beyond the diagonal of every
+            // query < T (masked), and rows of queries past T are not written.
+            const f32x4 kb4 = *reinterpret_cast<const f32x4 *>(&bias_lds[kDPad + ld_col]);
+            const f32x4 vb4 = *reinterpret_cast<const f32x4 *>(&bias_lds[2 * kDPad + ld_col]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kpre[i] += kb4;
+                vpre[i] += vb4;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = ld_row + 16 * i;
@@ -449,8 +478,12 @@ attn_fwd16_kernel(const FwdParams a) {
         // is in flight already (kpre2); it moves up after this step's tile,
         // so that this tile's compute does not wait for its loads.
         if (!DEEP && pre_ok) {
-            load_tile(pbh, pkt, kpre, vpre);
+            load_tile(pbh, pkt, kpre, vpre, bpre);
             pre_ok = advance(pit, pkt, pbh, pj);
+        }
+        if (biased && kt == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) qr[c] += *reinterpret_cast<const f32x4 *>(&bias_lds[16 * g + 4 * c]);
         }
 
         if (!diag) {
@@ -483,8 +516,9 @@ attn_fwd16_kernel(const FwdParams a) {
                 kpre[i] = kpre2[i];
                 vpre[i] = vpre2[i];
             }
+            bpre = bpre2;
             pre_ok = advance(pit, pkt, pbh, pj);
-            if (pre_ok) load_tile(pbh, pkt, kpre2, vpre2);
+            if (pre_ok) load_tile(pbh, pkt, kpre2, vpre2, bpre2);
         }
         if (!advance(it, kt, bh, jq)) break;
         b = bh / a.H;

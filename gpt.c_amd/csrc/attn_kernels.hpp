@@ -52,6 +52,10 @@ struct FwdParams {
     bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
     GridOrder order;      // grid order of the 32-row kernel (set by launch_attn_fwd)
     BlockSched sched;     // work lists of the 16-row kernel (set by launch_attn_fwd)
+    // Bias of the qkv Linear, added to q, k, v as they are loaded (16-row
+    // kernel only; nullptr: the input already holds x W^T + b).  Head h's
+    // entries are qb[h*D + d], kb[h*D + d], vb[h*D + d].
+    const float *qb, *kb, *vb;
 };
 
 struct BwdParams {
@@ -73,6 +77,14 @@ struct BwdParams {
     bool full;            // vec, D == kDPad and every head's rows span < 2^31 bytes
     GridOrder dq_order;   // grid order of the 32-row dq kernel (set by launch_attn_bwd)
     BlockSched sched;     // work lists of the 16-row dq kernel (set by launch_attn_bwd)
+    // The qkv Linear's bias folded into the loads (as in FwdParams; D = 64
+    // kernels only), and its gradient: per-workgroup column sums of the dq
+    // rows ((B*nqt) x C, one row per 64-query block) and of the dk | dv rows
+    // ((B*nkb) x 2C, one row per 128-key block), reduced in a fixed order into
+    // db (3C, accumulated) by the last kernel.  db == nullptr: none of this.
+    const float *qb, *kb, *vb;
+    float *dbq_part, *dbkv_part, *db;
+    int C;
 };
 
 // One KV-cache decode step (attn_decode.hip).

@@ -160,6 +160,12 @@ SIGNATURES = {
     "attention_decode_noalloc_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
     "gptc_decode_noalloc_scratch_floats": (ctypes.c_longlong, []),
     "gptc_retain_cuda": (None, [_vp]),
+    "gptc_attention_forward_bias": (TensorP, [_vp, TensorP, TensorP]),
+    "gptc_attention_backward_bias": (TensorP, [_vp, TensorP, TensorP, TensorP]),
+    "gptc_linear_forward_nobias": (TensorP, [_vp, TensorP]),
+    "gptc_linear_backward_nodb": (TensorP, [_vp, TensorP]),
+    "gptc_attention_forward_qkv_bias": (None, [TensorP, TensorP, TensorP, _ci, ctypes.POINTER(TensorP), TensorP]),
+    "gptc_attention_backward_qkv_bias": (None, [TensorP, ctypes.POINTER(TensorP), TensorP, _ci, TensorP, TensorP]),
     "gptc_attention_block_schedule": (_ci, [_ci, _ci, _ci, _ci, ctypes.POINTER(_ci), ctypes.POINTER(_ci), _ci,
                                              ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_ci)]),
     "saxpy_cuda": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),

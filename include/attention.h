@@ -37,6 +37,15 @@ typedef struct attention {
 
 attention_t *Attention(int n_embd, int n_heads, int block_size);
 
+/* No counterpart in the reference: the layer's forward and backward with
+ * the preceding qkv Linear's bias folded into the GPU kernels.  x holds
+ * x W^T without the bias; the backward returns dqkv as backward does and
+ * adds the bias gradient (its column sums) into db.  The library's own
+ * SelfAttention uses them (gpt.c adds the bias in the Linear,
+ * self_attention.c:59, and sums its gradient there). */
+tensor_t *gptc_attention_forward_bias(attention_t *attn, tensor_t *x, const tensor_t *bias);
+tensor_t *gptc_attention_backward_bias(attention_t *attn, tensor_t *global_grad, const tensor_t *bias, tensor_t *db);
+
 #ifdef __cplusplus
 }
 #endif

@@ -96,6 +96,28 @@ void attention_backward_cuda_kernel(
 );
 
 /*
+ * ---- the qkv Linear's bias folded into attention: no counterpart in the
+ * reference (gpt.c's SelfAttention adds it in the Linear, self_attention.c:59,
+ * and sums its gradient there, linear.c's backward) ----
+ *
+ * gptc_attention_forward_qkv_bias(input, bias, mask, n_heads, cache, output)
+ *   As attention_forward_cuda_kernel with the compact cache layout, where
+ *   input = x W^T holds the qkv Linear's product without its bias (3C): the
+ *   D = 64 kernels add the bias as they load q, k and v (the 75 MB bias
+ *   pass over the qkv activations at GPT-2 small's B=8 T=1024 disappears);
+ *   other head sizes have it added to the input in place first.
+ * gptc_attention_backward_qkv_bias(global_grad, cache, bias, n_heads, dout, db)
+ *   As attention_backward_cuda_kernel after that forward, and db (3C) +=
+ *   the column sums of dout (the bias gradient of the qkv Linear), formed
+ *   from per-workgroup sums in the kernels' epilogues and added in a fixed
+ *   order (deterministic).
+ */
+void gptc_attention_forward_qkv_bias(const tensor_t *input, const tensor_t *bias, const tensor_t *mask,
+                                     const int n_heads, tensor_t **cache, tensor_t *output);
+void gptc_attention_backward_qkv_bias(const tensor_t *global_grad, tensor_t **cache, const tensor_t *bias,
+                                      const int n_heads, tensor_t *dout, tensor_t *db);
+
+/*
  * ---- the rest of gpt.c's GPU back end (the other layers of the model) ----
  * Same names, arguments and meaning as the CUDA entry points they replace;
  * the semantics are those of gpt.c's CPU kernels (kernels/src/cpu/), which

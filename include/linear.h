@@ -39,6 +39,14 @@ typedef struct linear {
 
 linear_t *Linear(const int in_features, const int out_features, const int use_bias);
 
+/* No counterpart in the reference: forward and backward without the bias
+ * term, for a consumer that folds the bias into its own kernels (the
+ * library's SelfAttention, with the fused attention).  forward: x W^T,
+ * caching x as forward does; backward: dx = g W and dW += g^T x as backward
+ * does, leaving db to the caller; it consumes g and the cache. */
+tensor_t *gptc_linear_forward_nobias(linear_t *linear, tensor_t *x);
+tensor_t *gptc_linear_backward_nodb(linear_t *linear, tensor_t *global_grad);
+
 #ifdef __cplusplus
 }
 #endif

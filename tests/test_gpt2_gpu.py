@@ -129,13 +129,21 @@ def test_gpt2_training_steps_match_oracle(rt, oracle, V, block, L, H, C, B, T):
     compare_steps(names, gpu, ref)
 
 
-def test_self_attention_block_matches_oracle(rt, oracle):
+@pytest.mark.parametrize("B,T,C,H", [
+    (4, 256, 768, 12),  # GPT-2 small's widths: the qkv bias folded into the D = 64 kernels
+    (2, 100, 256, 4),   # short heads (T <= 128): folded, P recomputed in dk/dv
+    (1, 300, 128, 2),   # ragged T, folded
+    (2, 77, 96, 4),     # D = 24: the bias is added to the qkv activations instead
+])
+def test_self_attention_block_matches_oracle(rt, oracle, B, T, C, H):
     """SelfAttention (self_attention.c:47-83): forward and backward through
-    the library's layer objects vs the oracle's Linear -> attention -> Linear."""
+    the library's layer objects vs the oracle's Linear -> attention -> Linear.
+    On the GPU the layer folds the qkv Linear's bias into the attention
+    kernels (and its gradient into their epilogues); the oracle adds it in
+    the Linear, as gpt.c does."""
     import oracle as oracle_mod
     ops = oracle_mod.Ops(oracle)
-    B, T, C, H = 4, 256, 768, 12
-    rng = np.random.default_rng(5)
+    rng = np.random.default_rng(5 + T)
     Wq, bq = (rng.standard_normal((3 * C, C)) * 0.02).astype(np.float32), (rng.standard_normal(3 * C) * 0.1).astype(np.float32)
     Wp, bp = (rng.standard_normal((C, C)) * 0.02).astype(np.float32), (rng.standard_normal(C) * 0.1).astype(np.float32)
     x = rng.standard_normal((B, T, C)).astype(np.float32)
