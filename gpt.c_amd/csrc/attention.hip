@@ -39,9 +39,9 @@ bool full_tiles(const Dims &d, std::initializer_list<uint32_t> strides) {
 
 void check_head_size(const Dims &d) {
     CHECK_ERROR(d.H <= 0 || d.C % d.H != 0, "Expected C = %d to be divisible by n_heads = %d.", d.C, d.H);
-    CHECK_ERROR(d.D < 1 || d.D > gptc::kDPad,
+    CHECK_ERROR(d.D < 1 || d.D > 2 * gptc::kDPad,
                 "Head size %d is not supported by the GPU attention kernels (1 <= n_embd / n_heads <= %d).", d.D,
-                gptc::kDPad);
+                2 * gptc::kDPad);
 }
 
 // Views of q, k, v inside a (B, T, 3C) qkv tensor.

@@ -51,8 +51,10 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) 
         const float *o = a.o.p + b * a.o.sb + t * a.o.st + h * a.o.sh;
         const float *g = a.dout.p + b * a.dout.sb + t * a.dout.st + h * a.dout.sh;
         if (VEC) {
-            const f32x4 x = load4<true>(o, 4 * l16, a.D), y = load4<true>(g, 4 * l16, a.D);
-            sum = x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+            for (int d = 4 * l16; d < a.D; d += 64) {
+                const f32x4 x = load4<true>(o, d, a.D), y = load4<true>(g, d, a.D);
+                sum += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+            }
         } else {
             for (int d = l16; d < a.D; d += 16) sum = fmaf(o[d], g[d], sum);
         }
@@ -70,11 +72,23 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) 
 // from LDS as A operands, this lane's K row in registers as B operands) and
 // the causal mask applied per element; one workgroup per head at T <= 128,
 // so the kernel may use the registers of one wave per SIMD.
-template <bool VEC, bool FULL, bool RECOMP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RECOMP ? 1 : 2, RECOMP ? 1 : 2))) void
+//
+// DP: the head size the kernel is built for, 64 (D <= 64, the only choice
+// with FULL) or 128 (64 < D <= 128: one wave per SIMD, 64 more registers
+// per lane for V and as many for each of dK and dV).
+template <bool VEC, bool FULL, bool RECOMP, int DP = kDPad>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RECOMP || DP > kDPad ? 1 : 2,
+                                                                     RECOMP || DP > kDPad ? 1 : 2))) void
 attn_bwd_dkdv_kernel(const BwdParams a) {
-    __shared__ __attribute__((aligned(16))) float q_lds[kBwdBQ * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float do_lds[kBwdBQ * kLdsStride];
+    static_assert(!FULL || DP == kDPad, "FULL kernels are built for D == 64");
+    constexpr int LS = DP + 4;         // LDS row stride (floats)
+    constexpr int NJ = DP / 8;         // reduction steps of 8 dims (4 per lane half)
+    constexpr int NDB = DP / 32;       // 32-dim blocks of dK and dV
+    constexpr int TPR = DP / 4;        // tile-load threads per row (a float4 each)
+    constexpr int RPP = 256 / TPR;     // tile rows per load pass
+    constexpr int NLD = kBwdBQ / RPP;  // load passes per 64-query tile
+    __shared__ __attribute__((aligned(16))) float q_lds[kBwdBQ * LS];
+    __shared__ __attribute__((aligned(16))) float do_lds[kBwdBQ * LS];
     // Per-query statistics of the tile, one entry per thread: [0, 128) the
     // factors f of P = P' * f for the workgroup's two 64-key tiles
     // ([key tile][query]; RECOMP: [0, 64) LSE log2(e), +inf past T),
@@ -111,24 +125,24 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     const float *pm_h = a.pm + static_cast<uint32_t>(bh) * a.nqt * T;
 
     // V row of this lane's key, dims 8j + 4hf + c: B operand of dP = dO V^T.
-    f32x4 vr[8];
+    f32x4 vr[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) vr[j] = k_ok ? load4<VEC>(Vh + my_k * a.v.st, 8 * j + 4 * hf, D) : zero4();
+    for (int j = 0; j < NJ; ++j) vr[j] = k_ok ? load4<VEC>(Vh + my_k * a.v.st, 8 * j + 4 * hf, D) : zero4();
     // RECOMP: the K row of this lane's key, dims 8j + 4hf + c: B operand of S = Q K^T.
-    f32x4 kr[RECOMP ? 8 : 1];
+    f32x4 kr[RECOMP ? NJ : 1];
     if (RECOMP) {
         const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) kr[j] = k_ok ? load4<VEC>(Kh + my_k * a.k.st, 8 * j + 4 * hf, D) : zero4();
+        for (int j = 0; j < NJ; ++j) kr[j] = k_ok ? load4<VEC>(Kh + my_k * a.k.st, 8 * j + 4 * hf, D) : zero4();
     }
     // The qkv bias (FULL only): added to this key's V (and K) row here, to
     // the Q tiles through qb_lds.  Keys past T keep a zero row.
     const bool biased = FULL && a.qb != nullptr;
-    f32x4 vbias[8], kbias[RECOMP ? 8 : 1];
+    f32x4 vbias[NJ], kbias[RECOMP ? NJ : 1];
     f32x4 qb4 = zero4();
     if (biased) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             vbias[j] = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 8 * j + 4 * hf);
             if (RECOMP) kbias[j] = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + 8 * j + 4 * hf);
         }
@@ -140,7 +154,7 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     if (biased) {
         if (k_ok) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < NJ; ++j) {
                 vr[j] += vbias[j];
                 if (RECOMP) kr[j] += kbias[j];
             }
@@ -150,16 +164,16 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 
     const int qt0 = k_blk0 / kBwdBQ;
     const int n_qt = a.nqt;
-    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    const int ld_row = tid / TPR, ld_col = 4 * (tid % TPR);
     const auto q_rows = head_rows(Qh, T, a.q.st);
     const auto do_rows = head_rows(dOh, T, a.dout.st);
-    f32x4 qpre[4], dpre[4];
+    f32x4 qpre[NLD], dpre[NLD];
     float st0 = 0.0f, st1 = 0.0f;
     bool st_ok = false;
     auto prefetch = [&](int qt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = qt * kBwdBQ + ld_row + 16 * i;
+        for (int i = 0; i < NLD; ++i) {
+            const int q = qt * kBwdBQ + ld_row + RPP * i;
             if (FULL) {
                 qpre[i] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + ld_col);
                 dpre[i] = buffer_load4(do_rows, static_cast<uint32_t>(q) * a.dout.st + ld_col);
@@ -208,8 +222,9 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     };
     if (qt0 < n_qt) load_p(qt0, 0);
 
-    f32x16 acc_dk[2] = {zero16(), zero16()};
-    f32x16 acc_dv[2] = {zero16(), zero16()};
+    f32x16 acc_dk[NDB], acc_dv[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc_dk[db] = acc_dv[db] = zero16();
 
     for (int qt = qt0; qt < n_qt; ++qt) {
         __syncthreads();
@@ -218,13 +233,13 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
             // their P is 0 (f = 0, or the +inf LSE of RECOMP), so they add nothing.
             const f32x4 qb = *reinterpret_cast<const f32x4 *>(&qb_lds[ld_col]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) qpre[i] += qb;
+            for (int i = 0; i < NLD; ++i) qpre[i] += qb;
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = ld_row + 16 * i;
-            *reinterpret_cast<f32x4 *>(&q_lds[row * kLdsStride + ld_col]) = qpre[i];
-            *reinterpret_cast<f32x4 *>(&do_lds[row * kLdsStride + ld_col]) = dpre[i];
+        for (int i = 0; i < NLD; ++i) {
+            const int row = ld_row + RPP * i;
+            *reinterpret_cast<f32x4 *>(&q_lds[row * LS + ld_col]) = qpre[i];
+            *reinterpret_cast<f32x4 *>(&do_lds[row * LS + ld_col]) = dpre[i];
         }
         // Unconditional, so that no exec-masked branch sits between the loads
         // and their uses (branches make the wait counts conservative).
@@ -246,9 +261,9 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
             if (need) {
                 // dP (queries x keys) for this 32-query half.
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
+                for (int j = 0; j < NJ; ++j) {
                     const f32x4 da = *reinterpret_cast<const f32x4 *>(
-                        &do_lds[(32 * qb + l32) * kLdsStride + 8 * j + 4 * hf]);
+                        &do_lds[(32 * qb + l32) * LS + 8 * j + 4 * hf]);
 #pragma unroll
                     for (int c = 0; c < 4; ++c) dp = mfma32(da[c], vr[j][c], dp);
                 }
@@ -256,9 +271,9 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
                     // S (queries x keys) for this half, then P with the causal mask.
                     s = zero16();
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
+                    for (int j = 0; j < NJ; ++j) {
                         const f32x4 qa = *reinterpret_cast<const f32x4 *>(
-                            &q_lds[(32 * qb + l32) * kLdsStride + 8 * j + 4 * hf]);
+                            &q_lds[(32 * qb + l32) * LS + 8 * j + 4 * hf]);
 #pragma unroll
                         for (int c = 0; c < 4; ++c) s = mfma32(qa[c], kr[j][c], s);
                     }
@@ -311,14 +326,11 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int row = 32 * qb + 8 * g + 4 * hf + c;
-                    const float d0 = do_lds[row * kLdsStride + l32];
-                    const float d1 = do_lds[row * kLdsStride + 32 + l32];
-                    const float q0v = q_lds[row * kLdsStride + l32];
-                    const float q1v = q_lds[row * kLdsStride + 32 + l32];
-                    acc_dv[0] = mfma32(s[4 * g + c], d0, acc_dv[0]);
-                    acc_dv[1] = mfma32(s[4 * g + c], d1, acc_dv[1]);
-                    acc_dk[0] = mfma32(dp[4 * g + c], q0v, acc_dk[0]);
-                    acc_dk[1] = mfma32(dp[4 * g + c], q1v, acc_dk[1]);
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        acc_dv[db] = mfma32(s[4 * g + c], do_lds[row * LS + 32 * db + l32], acc_dv[db]);
+                        acc_dk[db] = mfma32(dp[4 * g + c], q_lds[row * LS + 32 * db + l32], acc_dk[db]);
+                    }
                 }
         }
     }
@@ -328,7 +340,7 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     float *dKh = a.dk.p + b * a.dk.sb + h * a.dk.sh;
     float *dVh = a.dv.p + b * a.dv.sb + h * a.dv.sh;
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
+    for (int db = 0; db < NDB; ++db) {
         const int dim = 32 * db + l32;
         if (dim >= D) continue;
 #pragma unroll
@@ -369,10 +381,16 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     }
 }
 
-// ---- dQ = dS K / sqrt(D) from the stored dS tiles ----
-template <bool VEC, bool FULL>
+// ---- dQ = dS K / sqrt(D) from the stored dS tiles (head sizes other than 64) ----
+// DP: the head size the kernel is built for, 64 or 128 (as for dk/dv).
+template <bool VEC, int DP>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
-    __shared__ __attribute__((aligned(16))) float k_lds[kBwdBN * kLdsStride];
+    constexpr int LS = DP + 4;         // LDS row stride (floats)
+    constexpr int NDB = DP / 32;       // 32-dim blocks of dQ
+    constexpr int TPR = DP / 4;        // tile-load threads per row (a float4 each)
+    constexpr int RPP = 256 / TPR;     // tile rows per load pass
+    constexpr int NLD = kBwdBN / RPP;  // load passes per 64-key tile
+    __shared__ __attribute__((aligned(16))) float k_lds[kBwdBN * LS];
 
     const int tid = threadIdx.x;
     // The wave index is made visibly uniform (an SGPR): branches on it are then
@@ -393,7 +411,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
     const bool wave_on = qw0 < T;
 
     const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
-    const auto k_rows = head_rows(Kh, T, a.k.st);
     // This lane's dS row (query my_q) inside its 64-query tile: key block kb32
     // starts kb32 * 2048 floats after the (uniform) tile base; keys
     // 8g + 4hf + c come as float4 g.
@@ -403,17 +420,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
 
     const int kv_end = min(T, q_blk0 + kBwdBM);
     const int n_tiles = (kv_end + kBwdBN - 1) / kBwdBN;
-    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
-    f32x4 kpre[4];
+    const int ld_row = tid / TPR, ld_col = 4 * (tid % TPR);
+    f32x4 kpre[NLD];
     f32x4 dsn[2][4];
     auto prefetch = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = kt * kBwdBN + ld_row + 16 * i;
-            if (FULL)
-                kpre[i] = buffer_load4(k_rows, static_cast<uint32_t>(key) * a.k.st + ld_col);
-            else
-                kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
+        for (int i = 0; i < NLD; ++i) {
+            const int key = kt * kBwdBN + ld_row + RPP * i;
+            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
         }
         // Key blocks past this wave's diagonal (all of dS zero there) or wholly
         // past T are never written by the dk/dv kernel: read nothing from them.
@@ -429,12 +443,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
     };
     prefetch(0);
 
-    f32x16 acc_dq[2] = {zero16(), zero16()};
+    f32x16 acc_dq[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc_dq[db] = zero16();
     for (int kt = 0; kt < n_tiles; ++kt) {
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<f32x4 *>(&k_lds[(ld_row + 16 * i) * kLdsStride + ld_col]) = kpre[i];
+        for (int i = 0; i < NLD; ++i)
+            *reinterpret_cast<f32x4 *>(&k_lds[(ld_row + RPP * i) * LS + ld_col]) = kpre[i];
         __syncthreads();
         f32x4 dsc[2][4];
 #pragma unroll
@@ -452,17 +468,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int row = 32 * kb + 8 * g + 4 * hf + c;
-                    const float ka0 = k_lds[row * kLdsStride + l32];
-                    const float ka1 = k_lds[row * kLdsStride + 32 + l32];
-                    acc_dq[0] = mfma32(ka0, dsc[kb][g][c], acc_dq[0]);
-                    acc_dq[1] = mfma32(ka1, dsc[kb][g][c], acc_dq[1]);
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+                        acc_dq[db] = mfma32(k_lds[row * LS + 32 * db + l32], dsc[kb][g][c], acc_dq[db]);
                 }
     }
 
     if (my_q >= T) return;
     float *dqrow = a.dq.p + b * a.dq.sb + my_q * a.dq.st + h * a.dq.sh;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             f32x4 val;
@@ -653,11 +668,19 @@ size_t bwd_ds_floats(int B, int H, int T) {
 
 void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     BwdParams p = p_in;
-    // The grid order serves the 32-row dq kernel only (the 16-row one pairs blocks).
-    if (!p.full && p.vec)
-        p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<true, false>);
-    else if (!p.full)
-        p.dq_order = choose_grid_order(p.nqb, p.bh_pad, attn_bwd_dq_kernel<false, false>);
+    const bool wide = p.D > kDPad;  // 64 < D <= 128: the DP = 128 kernels
+    // The 32-row dq kernel for head sizes other than 64, and its grid order
+    // (the 16-row one runs work lists).
+    const void *dq_kern = nullptr;
+    if (!p.full) {
+        if (wide)
+            dq_kern = p.vec ? reinterpret_cast<const void *>(attn_bwd_dq_kernel<true, 2 * kDPad>)
+                            : reinterpret_cast<const void *>(attn_bwd_dq_kernel<false, 2 * kDPad>);
+        else
+            dq_kern = p.vec ? reinterpret_cast<const void *>(attn_bwd_dq_kernel<true, kDPad>)
+                            : reinterpret_cast<const void *>(attn_bwd_dq_kernel<false, kDPad>);
+        p.dq_order = choose_grid_order(p.nqb, p.bh_pad, dq_kern);
+    }
     const dim3 block(256);
     const int rows = p.B * p.T * p.H;
     const dim3 grid_d((rows + 15) / 16), grid_k(p.nkb * p.bh_pad), grid_q(p.nqb * p.bh_pad);
@@ -675,6 +698,10 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
         attn_bwd_dkdv_kernel<true, true, true><<<grid_k, block, 0, stream>>>(p);
     else if (p.full)
         attn_bwd_dkdv_kernel<true, true, false><<<grid_k, block, 0, stream>>>(p);
+    else if (wide && p.vec)
+        attn_bwd_dkdv_kernel<true, false, false, 2 * kDPad><<<grid_k, block, 0, stream>>>(p);
+    else if (wide)
+        attn_bwd_dkdv_kernel<false, false, false, 2 * kDPad><<<grid_k, block, 0, stream>>>(p);
     else if (p.vec)
         attn_bwd_dkdv_kernel<true, false, false><<<grid_k, block, 0, stream>>>(p);
     else
@@ -690,10 +717,10 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
                                         stream, &num_wg);
         attn_bwd_dq16_kernel<<<dim3(num_wg), block, 0, stream>>>(p);
     }
-    else if (p.vec)
-        attn_bwd_dq_kernel<true, false><<<grid_q, block, 0, stream>>>(p);
-    else
-        attn_bwd_dq_kernel<false, false><<<grid_q, block, 0, stream>>>(p);
+    else {
+        void *args[] = {&p};
+        hipCheck(hipLaunchKernel(dq_kern, grid_q, block, args, 0, stream));
+    }
     hipCheck(hipGetLastError());
     if (ev) hipCheck(hipEventRecord(ev[5], stream));
 }

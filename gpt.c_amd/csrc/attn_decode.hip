@@ -13,7 +13,7 @@
 // (b, h)).  For D == 64 with 16-byte cache rows the split-key kernels at the
 // end of this file run; the kernel first below serves the other head sizes:
 // one 1024-thread workgroup (16 waves) per (b, h), with as many row loads in
-// flight as the registers allow.
+// flight as the registers allow (head sizes up to 128).
 //   phase 1  thread per key: t_j = (q . k_j) log2(e)/sqrt(D) into LDS;
 //   phase 2  workgroup max m and sum l of p_j = exp2(t_j - m);
 //   phase 3  wave per key row, lane per dim: o = sum_j p_j v_j (coalesced
@@ -49,10 +49,12 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 
 }  // namespace
 
+constexpr int kDecMaxD = 2 * kDPad;  // head sizes up to 128
+
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParams a) {
     extern __shared__ float dyn_lds[];  // scores: pos + 1 floats (L with a device-side position)
-    __shared__ float q_s[kDPad], k_s[kDPad], v_s[kDPad];
-    __shared__ float o_s[kDecWaves][kDPad];
+    __shared__ float q_s[kDecMaxD], k_s[kDecMaxD], v_s[kDecMaxD];
+    __shared__ float o_s[kDecWaves][kDecMaxD];
     __shared__ float red[kDecWaves];
 
     // A device-side position (graph replays) is checked here, since the host
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
     const float *row = a.qkv + static_cast<size_t>(b) * 3 * a.C + h * D;
     float *kc = a.k_cache + static_cast<size_t>(bh) * a.L * D;
     float *vc = a.v_cache + static_cast<size_t>(bh) * a.L * D;
-    if (tid < kDPad) {
+    if (tid < kDecMaxD) {
         const bool ok = tid < D;
         q_s[tid] = ok ? row[tid] : 0.0f;
         const float kn = ok ? row[a.C + tid] : 0.0f, vn = ok ? row[2 * a.C + tid] : 0.0f;
@@ -92,8 +94,12 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
     for (int j = tid; j < n; j += kDecThreads) {
         float acc = 0.0f;
         if (j == pos) {
+            if (D <= kDPad) {
 #pragma unroll
-            for (int d = 0; d < kDPad; ++d) acc = fmaf(q[d], k_s[d], acc);
+                for (int d = 0; d < kDPad; ++d) acc = fmaf(q[d], k_s[d], acc);
+            } else {
+                for (int d = 0; d < D; ++d) acc = fmaf(q_s[d], k_s[d], acc);
+            }
         } else if (a.full) {
             const f32x4 *kr = reinterpret_cast<const f32x4 *>(kc + static_cast<size_t>(j) * D);
 #pragma unroll
@@ -123,25 +129,29 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParam
     }
     const float l = block_reduce(l_part, red, false);  // its barriers also publish the p_j
 
-    // Phase 3: wave w takes keys w, w + 16, ...; lane = dim.
+    // Phase 3: wave w takes keys w, w + 16, ...; lane = dim (and dim + 64
+    // for head sizes past 64).
     constexpr int kUnroll = 8;
-    float o = 0.0f;
-    if (lane < D) {
-        int j = w;
-        // Keys below pos come from the cache, kUnroll rows in flight per lane.
-        for (; j + (kUnroll - 1) * kDecWaves < pos; j += kUnroll * kDecWaves) {
-            float v[kUnroll];
+    for (int dim = lane; dim < kDecMaxD; dim += 64) {
+        float o = 0.0f;
+        if (dim < D) {
+            int j = w;
+            // Keys below pos come from the cache, kUnroll rows in flight per lane.
+            for (; j + (kUnroll - 1) * kDecWaves < pos; j += kUnroll * kDecWaves) {
+                float v[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) v[u] = vc[static_cast<size_t>(j + u * kDecWaves) * D + lane];
+                for (int u = 0; u < kUnroll; ++u) v[u] = vc[static_cast<size_t>(j + u * kDecWaves) * D + dim];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) o = fmaf(dyn_lds[j + u * kDecWaves], v[u], o);
+                for (int u = 0; u < kUnroll; ++u) o = fmaf(dyn_lds[j + u * kDecWaves], v[u], o);
+            }
+            for (; j < n; j += kDecWaves) {
+                const float v = (j == pos) ? v_s[dim] : vc[static_cast<size_t>(j) * D + dim];
+                o = fmaf(dyn_lds[j], v, o);
+            }
         }
-        for (; j < n; j += kDecWaves) {
-            const float v = (j == pos) ? v_s[lane] : vc[static_cast<size_t>(j) * D + lane];
-            o = fmaf(dyn_lds[j], v, o);
-        }
+        o_s[w][dim] = o;
+        if (D <= kDPad) break;
     }
-    o_s[w][lane] = o;
     __syncthreads();
     if (tid < D) {
         float y = o_s[0][tid];

@@ -31,12 +31,21 @@ constexpr int kFwdBM = 128;  // queries per workgroup
 constexpr int kFwdBN = 64;   // keys per LDS tile
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 
-// FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the K/V tile loads
-// then go through bounds-checked buffer resources (no branches, no row tests).
-template <bool VEC, bool FULL, bool PERM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_fwd_kernel(const FwdParams a) {
-    __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
+// DP: the head size the kernel is built for, 64 (D <= 64) or 128 (64 < D <=
+// 128); a smaller D is zero-padded in registers.  DP = 128 keeps 64 more
+// registers per lane and twice the LDS per tile: one workgroup per CU, one
+// wave per SIMD.
+template <bool VEC, int DP, bool PERM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 3 : 1, DP == 64 ? 3 : 1))) void
+attn_fwd_kernel(const FwdParams a) {
+    constexpr int LS = DP + 4;       // LDS row stride (floats)
+    constexpr int NJ = DP / 8;       // reduction steps of 8 dims (4 per lane half)
+    constexpr int NDB = DP / 32;     // 32-dim blocks of the output
+    constexpr int TPR = DP / 4;      // tile-load threads per row (a float4 each)
+    constexpr int RPP = 256 / TPR;   // tile rows per load pass
+    constexpr int NLD = kFwdBN / RPP;  // load passes per 64-key tile
+    __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * LS];
+    __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * LS];
 
     const int tid = threadIdx.x;
     // The wave index is made visibly uniform (an SGPR): branches on it are then
@@ -44,8 +53,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
 
-    // Query blocks in the XCD- and CU-aware order of grid_order.hpp (three
-    // workgroups per CU, the whole C2 grid resident at once).
+    // Query blocks in the XCD- and CU-aware order of grid_order.hpp.
     int blk, bh;
     grid_position(a.order, a.nqb, a.bh_pad, blk, bh);
     if (bh >= a.B * a.H) return;
@@ -62,35 +70,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
 
     // Q row of this lane's query, dims 8j + 4hf + c, as B operands.
-    f32x4 qr[8];
+    f32x4 qr[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < NJ; ++j)
         qr[j] = (my_q < T) ? load4<VEC>(Qh + my_q * a.q.st, 8 * j + 4 * hf, D) : zero4();
     if (PERM && my_q < T) {
         float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * D;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) store4<VEC>(dst, 8 * j + 4 * hf, D, qr[j]);
+        for (int j = 0; j < NJ; ++j) store4<VEC>(dst, 8 * j + 4 * hf, D, qr[j]);
     }
 
     const int kv_end = min(T, q_blk0 + kFwdBM);
     const int n_tiles = (kv_end + kFwdBN - 1) / kFwdBN;
 
-    // Cooperative tile load: thread covers rows (tid>>4) + 16i, dims 4*(tid&15).
-    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
-    const auto k_rows = head_rows(Kh, T, a.k.st);
-    const auto v_rows = head_rows(Vh, T, a.v.st);
-    f32x4 kpre[4], vpre[4];
+    // Cooperative tile load: thread covers rows tid / TPR + RPP i, dims 4 (tid % TPR).
+    const int ld_row = tid / TPR, ld_col = 4 * (tid % TPR);
+    f32x4 kpre[NLD], vpre[NLD];
     auto prefetch = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = kt * kFwdBN + ld_row + 16 * i;
-            if (FULL) {
-                kpre[i] = buffer_load4(k_rows, static_cast<uint32_t>(key) * a.k.st + ld_col);
-                vpre[i] = buffer_load4(v_rows, static_cast<uint32_t>(key) * a.v.st + ld_col);
-            } else {
-                kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
-                vpre[i] = (key < T) ? load4<VEC>(Vh + key * a.v.st, ld_col, D) : zero4();
-            }
+        for (int i = 0; i < NLD; ++i) {
+            const int key = kt * kFwdBN + ld_row + RPP * i;
+            kpre[i] = (key < T) ? load4<VEC>(Kh + key * a.k.st, ld_col, D) : zero4();
+            vpre[i] = (key < T) ? load4<VEC>(Vh + key * a.v.st, ld_col, D) : zero4();
         }
     };
     prefetch(0);
@@ -98,21 +99,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const float c2 = a.scale_log2;
     float m_run = -INFINITY;  // running max of s * c2 for this lane's query
     float l_run = 0.0f;       // this half-wave's share of the running sum
-    f32x16 acc_o[2] = {zero16(), zero16()};
+    f32x16 acc_o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc_o[db] = zero16();
 
     for (int kt = 0; kt < n_tiles; ++kt) {
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = ld_row + 16 * i;
-            *reinterpret_cast<f32x4 *>(&k_lds[row * kLdsStride + ld_col]) = kpre[i];
-            *reinterpret_cast<f32x4 *>(&v_lds[row * kLdsStride + ld_col]) = vpre[i];
+        for (int i = 0; i < NLD; ++i) {
+            const int row = ld_row + RPP * i;
+            *reinterpret_cast<f32x4 *>(&k_lds[row * LS + ld_col]) = kpre[i];
+            *reinterpret_cast<f32x4 *>(&v_lds[row * LS + ld_col]) = vpre[i];
         }
         if (PERM && kt * kFwdBN >= q_blk0) {
             // Keys of this workgroup's own block: emit the permuted copies.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kt * kFwdBN + ld_row + 16 * i;
+            for (int i = 0; i < NLD; ++i) {
+                const int key = kt * kFwdBN + ld_row + RPP * i;
                 if (key < T) {
                     const uint32_t off = (static_cast<uint32_t>(bh) * T + key) * D;
                     store4<VEC>(a.kp + off, ld_col, D, kpre[i]);
@@ -129,9 +132,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         // S^T (keys x queries) for two 32-key blocks.
         f32x16 s[2] = {zero16(), zero16()};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&k_lds[l32 * kLdsStride + 8 * j + 4 * hf]);
-            const f32x4 kb = *reinterpret_cast<const f32x4 *>(&k_lds[(32 + l32) * kLdsStride + 8 * j + 4 * hf]);
+        for (int j = 0; j < NJ; ++j) {
+            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&k_lds[l32 * LS + 8 * j + 4 * hf]);
+            const f32x4 kb = *reinterpret_cast<const f32x4 *>(&k_lds[(32 + l32) * LS + 8 * j + 4 * hf]);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 s[0] = mfma32(ka[c], qr[j][c], s[0]);
@@ -170,10 +173,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             const float alpha = fast_exp2(m_run - m_use);
             l_run *= alpha;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc_o[0][r] *= alpha;
-                acc_o[1][r] *= alpha;
-            }
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc_o[db][r] *= alpha;
             m_run = m_new;
         }
         const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
@@ -212,10 +214,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int row = 32 * kb + 8 * g + 4 * hf + c;
-                    const float va0 = v_lds[row * kLdsStride + l32];
-                    const float va1 = v_lds[row * kLdsStride + 32 + l32];
-                    acc_o[0] = mfma32(va0, s[kb][4 * g + c], acc_o[0]);
-                    acc_o[1] = mfma32(va1, s[kb][4 * g + c], acc_o[1]);
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+                        acc_o[db] = mfma32(v_lds[row * LS + 32 * db + l32], s[kb][4 * g + c], acc_o[db]);
                 }
     }
 
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     float *orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh;
     float *o2row = a.o2 ? a.o2 + b * a.o.sb + my_q * a.o.st + h * a.o.sh : nullptr;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             f32x4 val;
@@ -553,27 +554,22 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
         if (ev) hipCheck(hipEventRecord(ev[1], stream));
         return;
     }
-    // The 32-row kernel: other head sizes and unaligned rows (FULL is the
-    // 16-row kernel's case above).
-    if (p.vec && perm)
-        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, false, true>);
-    else if (p.vec)
-        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<true, false, false>);
-    else if (perm)
-        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<false, false, true>);
-    else
-        p.order = choose_grid_order(p.nqb, p.bh_pad, attn_fwd_kernel<false, false, false>);
+    // The 32-row kernel: other head sizes and unaligned rows (the 16-row
+    // kernel above serves D == 64 with 16-byte rows).
+    auto pick = [&](auto dp_c) {
+        constexpr int DP = decltype(dp_c)::value;
+        if (p.vec && perm) return reinterpret_cast<const void *>(attn_fwd_kernel<true, DP, true>);
+        if (p.vec) return reinterpret_cast<const void *>(attn_fwd_kernel<true, DP, false>);
+        if (perm) return reinterpret_cast<const void *>(attn_fwd_kernel<false, DP, true>);
+        return reinterpret_cast<const void *>(attn_fwd_kernel<false, DP, false>);
+    };
+    const bool wide = p.D > kDPad;
+    const void *kern = wide ? pick(IntC<2 * kDPad>{}) : pick(IntC<kDPad>{});
+    p.order = choose_grid_order(p.nqb, p.bh_pad, kern);
     const dim3 grid(p.nqb * p.bh_pad), block(256);
-    const bool vec = p.vec;
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
-    if (vec && perm)
-        attn_fwd_kernel<true, false, true><<<grid, block, 0, stream>>>(p);
-    else if (vec)
-        attn_fwd_kernel<true, false, false><<<grid, block, 0, stream>>>(p);
-    else if (perm)
-        attn_fwd_kernel<false, false, true><<<grid, block, 0, stream>>>(p);
-    else
-        attn_fwd_kernel<false, false, false><<<grid, block, 0, stream>>>(p);
+    void *args[] = {&p};
+    hipCheck(hipLaunchKernel(kern, grid, block, args, 0, stream));
     hipCheck(hipGetLastError());
     if (ev) hipCheck(hipEventRecord(ev[1], stream));
 }

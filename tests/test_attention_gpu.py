@@ -93,12 +93,46 @@ SMALL = [  # (B, T, C, H)
     (1, 257, 48, 1),       # D = 48
     (2, 300, 48, 3),       # D = 16
     (1, 511, 768, 12),     # C4's longest window shape at B = 1
+    (2, 77, 384, 4),       # D = 96 (kernels built for 128 padded dims)
+    (1, 200, 768, 6),      # D = 128
+    (2, 33, 260, 4),       # D = 65 (128 padded dims, ragged)
 ]
 
 
 @pytest.mark.parametrize("B,T,C,H", SMALL)
 def test_small_shapes_fwd_bwd(rt, oracle, B, T, C, H):
     compare_with_oracle(rt, oracle, B, T, C, H)
+
+
+def test_head_size_128_full_length(rt, oracle):
+    """D = 128 over 16 key tiles (T = 1024): the 128-dim forward, dk/dv and dq kernels."""
+    compare_with_oracle(rt, oracle, 1, 1024, 1024, 8)
+
+
+def test_head_size_past_128_is_refused():
+    """Head sizes the kernels are not built for end the process with gpt.c's error
+    report before any launch (a host-side check)."""
+    import os
+    import subprocess
+    import sys
+    import textwrap
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpt.c_amd")
+    code = textwrap.dedent(f"""
+        import sys
+        sys.path.insert(0, {pkg!r})
+        import numpy as np
+        import gptc
+        lib = gptc.load()
+        rt = gptc.Runtime(lib)
+        rt.init()
+        layer = gptc.AttentionLayer(rt, 516, 2, 4)
+        layer.to(gptc.CUDA)
+        layer.forward(rt.from_numpy(np.zeros((1, 4, 3 * 516), np.float32)))
+        print('survived')
+    """)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1 and "survived" not in r.stdout, r.stderr
+    assert "Head size 258 is not supported" in r.stderr and "[ERROR]" in r.stderr
 
 
 def test_mask_block_larger_than_T(rt, oracle):

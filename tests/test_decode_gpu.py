@@ -67,6 +67,8 @@ def decode_all(rt, x, H, L=None):
     (2, 70, 96, 4, 70),      # D = 24 (plain loads)
     (2, 9, 6, 2, 16),        # D = 3 (gpt.c's tests/test_self_attention.c shape class)
     (1, 64, 100, 25, 64),    # H = 25, D = 4
+    (2, 33, 192, 2, 40),     # D = 96
+    (1, 40, 256, 2, 48),     # D = 128
 ])
 def test_decode_every_position(rt, oracle, B, T, C, H, L):
     x = rt.normal((B, T, 3 * C), 1337)

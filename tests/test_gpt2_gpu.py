@@ -134,6 +134,7 @@ def test_gpt2_training_steps_match_oracle(rt, oracle, V, block, L, H, C, B, T):
     (2, 100, 256, 4),   # short heads (T <= 128): folded, P recomputed in dk/dv
     (1, 300, 128, 2),   # ragged T, folded
     (2, 77, 96, 4),     # D = 24: the bias is added to the qkv activations instead
+    (2, 64, 256, 2),    # D = 128 (the 128-dim kernels), bias added to the activations
 ])
 def test_self_attention_block_matches_oracle(rt, oracle, B, T, C, H):
     """SelfAttention (self_attention.c:47-83): forward and backward through
