@@ -75,7 +75,7 @@ int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 //   [y copy (B*T*C) | log-sum-exp (B*H*T)]   reference cache layout only
 //   delta (B*H*T)                            written by the backward
 //   m (B*H*nqt*T)                            per-tile row maxima of P'
-//   db partials (B*nqt*C + B*nkb*2C)        column sums of the dq | dk, dv
+//   db partials (B*nqt*C + B*2nkb*2C)       column sums of the dq | dk, dv
 //                                            rows (qkv bias folded in only)
 //   P' / dS blocks (bwd_ds_floats)           P' from forward, dS in backward
 struct StateLayout {
@@ -101,8 +101,8 @@ StateLayout state_layout(const Dims &d, bool reference_layout) {
     const int64_t nkb = (d.T + 127) / 128;
     s.dbq = off;
     off += align64(static_cast<int64_t>(d.B) * nqt * d.C);
-    s.dbkv = off;
-    off += align64(static_cast<int64_t>(d.B) * nkb * 2 * d.C);
+    s.dbkv = off;  // up to 2 nkb rows per batch row: split key blocks add one each
+    off += align64(static_cast<int64_t>(d.B) * 2 * nkb * 2 * d.C);
     s.p = off;
     off += static_cast<int64_t>(gptc::bwd_ds_floats(d.B, d.H, d.T));
     s.total = off;
@@ -332,6 +332,7 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
             aligned16(global_grad->t) && aligned16(dout->t);
     p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.dout.st});
     hipStream_t s = gptc_stream_checked();
+    gptc::bwd_split_plan(p);
     bool folded = false;
     if (bias != nullptr) {
         CHECK_ERROR(!compact, "The qkv bias can be folded in with the compact cache layout only.");
@@ -360,7 +361,7 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
         if (folded) {
             // db += the per-block column sums, in a fixed order.
             gptc::launch_add_column_partials(p.dbq_part, db->t, d.B * nqt, d.C, s);
-            gptc::launch_add_column_partials(p.dbkv_part, db->t + d.C, d.B * nkb, 2 * d.C, s);
+            gptc::launch_add_column_partials(p.dbkv_part, db->t + d.C, d.B * (nkb + p.nsplit), 2 * d.C, s);
         } else {
             gptc::launch_column_sum_add(dout->t, db->t, d.B * d.T, 3 * d.C, s);
         }

@@ -23,7 +23,13 @@
 //   attn_bwd_dq_kernel     query-parallel, other D: dQ^T += K^T dS^T.
 // The accumulator of the score product is directly the operand of the
 // gradient products (see the layout note in attn_common.hpp).
+#include <algorithm>
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
+#include <vector>
+
 #include "attn_common.hpp"
 #include "attn_kernels.hpp"
 #include "hip_check.hpp"
@@ -62,6 +68,11 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) 
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
     if (row < rows && l16 == 0) a.delta[(static_cast<uint32_t>(b) * a.H + h) * a.T + t] = sum;
+    // dK, dV rows of the split key blocks start at zero (D == 64, 16-byte rows).
+    if (VEC && row < rows && t < a.nsplit * kBwdBK) {
+        *reinterpret_cast<f32x4 *>(a.dk.p + b * a.dk.sb + t * a.dk.st + h * a.dk.sh + 4 * l16) = zero4();
+        *reinterpret_cast<f32x4 *>(a.dv.p + b * a.dv.sb + t * a.dv.st + h * a.dv.sh + 4 * l16) = zero4();
+    }
 }
 
 // ---- dK, dV (and the dS tiles) ----
@@ -107,8 +118,11 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
     const int bh = blockIdx.x % a.bh_pad;
     if (bh >= a.B * a.H) return;
-    // Low key blocks see the most queries: launch them first.
-    const int kb_idx = static_cast<int>(blockIdx.x / a.bh_pad);
+    // Grid row -> key block (and part of a split one); the longest work first.
+    const int row_idx = static_cast<int>(blockIdx.x / a.bh_pad);
+    const int slot = FULL && !RECOMP && a.nsplit > 0 ? a.slot[row_idx] : 2 * row_idx;
+    const int kb_idx = slot >> 1, part = slot & 1;
+    const bool split = FULL && !RECOMP && kb_idx < a.nsplit;
     const int b = bh / a.H, h = bh - b * a.H;
     const int T = a.T, D = a.D;
 
@@ -162,8 +176,11 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
         if (tid < kDPad / 4) *reinterpret_cast<f32x4 *>(&qb_lds[4 * tid]) = qb4;
     }
 
-    const int qt0 = k_blk0 / kBwdBQ;
+    // Query tiles [qt0, q_end): all from the diagonal on, or one part of them.
     const int n_qt = a.nqt;
+    const int qt_diag = k_blk0 / kBwdBQ, q_mid = qt_diag + (n_qt - qt_diag + 1) / 2;
+    const int qt0 = split && part ? q_mid : qt_diag;
+    const int q_end = split && !part ? q_mid : n_qt;
     const int ld_row = tid / TPR, ld_col = 4 * (tid % TPR);
     const auto q_rows = head_rows(Qh, T, a.q.st);
     const auto do_rows = head_rows(dOh, T, a.dout.st);
@@ -195,7 +212,7 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
         st0 = RECOMP ? dl_h[qc] : *(is_m ? pm_h + min(kt, n_qt - 1) * T + qc : dl_h + qc);
         st1 = lse_h[qc];
     };
-    if (qt0 < n_qt) prefetch(qt0);
+    if (qt0 < q_end) prefetch(qt0);
 
     // P' of one 32-query half, loaded one half ahead of its use: register r
     // holds query 8(r/4) + 4hf + r%4 of the half, key my_k (the accumulator
@@ -220,13 +237,13 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
     };
-    if (qt0 < n_qt) load_p(qt0, 0);
+    if (qt0 < q_end) load_p(qt0, 0);
 
     f32x16 acc_dk[NDB], acc_dv[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) acc_dk[db] = acc_dv[db] = zero16();
 
-    for (int qt = qt0; qt < n_qt; ++qt) {
+    for (int qt = qt0; qt < q_end; ++qt) {
         __syncthreads();
         if (biased) {
             // Q rows past T hold the bias too: their dO rows are zero and
@@ -302,8 +319,8 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
                 load_p(qt, 1);
                 // Issued after this half's P' is consumed, so that waiting for
                 // that P' never waits for these loads.
-                if (qt + 1 < n_qt) prefetch(qt + 1);
-            } else if (qt + 1 < n_qt) {
+                if (qt + 1 < q_end) prefetch(qt + 1);
+            } else if (qt + 1 < q_end) {
                 load_p(qt + 1, 0);
             }
             if (!need) continue;
@@ -347,8 +364,13 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
         for (int r = 0; r < 16; ++r) {
             const int key = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3);
             if (key < T) {
-                dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
-                dVh[key * a.dv.st + dim] = acc_dv[db][r];
+                if (split) {
+                    unsafeAtomicAdd(&dKh[key * a.dk.st + dim], acc_dk[db][r] * a.scale);
+                    unsafeAtomicAdd(&dVh[key * a.dv.st + dim], acc_dv[db][r]);
+                } else {
+                    dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
+                    dVh[key * a.dv.st + dim] = acc_dv[db][r];
+                }
             }
         }
     }
@@ -374,9 +396,11 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
         __syncthreads();
         if (tid < 2 * kDPad) {
             const float s = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
-            // Row (b, key block) of the (B*nkb) x 2C partials: dk part, then dv part.
+            // Row (b, key block or its part 1) of the (B*(nkb + nsplit)) x 2C
+            // partials: dk part, then dv part.
             const int col = (tid < kDPad ? 0 : a.C) + h * kDPad + (tid & (kDPad - 1));
-            a.dbkv_part[(static_cast<size_t>(b) * a.nkb + kb_idx) * 2 * a.C + col] = s;
+            const int prow = split && part ? a.nkb + kb_idx : kb_idx;
+            a.dbkv_part[(static_cast<size_t>(b) * (a.nkb + a.nsplit) + prow) * 2 * a.C + col] = s;
         }
     }
 }
@@ -661,6 +685,66 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
     }
 }
 
+namespace {
+
+// Key blocks are split, longest first, while the grid of key blocks and
+// parts still fits in the GPU's resident workgroup slots: a grid that leaves
+// CUs idle (B * H = 12 heads of T = 1024 make 96 workgroups for 512 slots)
+// is as long as its longest block, and halving the longest blocks halves it
+// (126 -> 70 us measured at B = 1, H = 12, T = 1024).  A grid that fills the
+// slots gains nothing from it (B = 8, H = 12: 204.8 -> 203.2 us with plain
+// stores timed in place of the adds) and would pay for the zeroing and the
+// atomic adds (+6 us), so it is not split.
+std::mutex g_split_mu;
+std::map<int, std::pair<int, int>> g_dkdv_slots;  // device -> (workgroups per CU, CUs)
+
+std::pair<int, int> dkdv_slots() {
+    int dev = 0;
+    hipCheck(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_split_mu);
+    auto it = g_dkdv_slots.find(dev);
+    if (it == g_dkdv_slots.end()) {
+        int per_cu = 0, cus = 0;
+        hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(attn_bwd_dkdv_kernel<true, true, false>), 256, 0));
+        hipCheck(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        it = g_dkdv_slots.emplace(dev, std::make_pair(std::max(1, per_cu), std::max(1, cus))).first;
+    }
+    return it->second;
+}
+
+}  // namespace
+
+int bwd_split_plan(BwdParams &p) {
+    p.nsplit = 0;
+    if (!p.full || p.nqt <= kShortHeadTiles) return 0;
+    const auto [per_cu, cus] = dkdv_slots();
+    const auto tiles = [&](int kb) { return p.nqt - 2 * kb; };  // query tiles of key block kb
+    const long long slots = static_cast<long long>(per_cu) * cus, bh = static_cast<long long>(p.B) * p.H;
+    int nsplit = 0;
+    while (nsplit < p.nkb && tiles(nsplit) >= 2 && p.nkb + nsplit + 1 <= kBwdMaxSlots &&
+           (p.nkb + nsplit + 1) * bh <= slots)
+        ++nsplit;
+    if (nsplit == 0) return 0;
+    // Grid rows longest first: part 0 of a split block takes the larger half.
+    struct Row {
+        int cost, kb, part;
+    };
+    std::vector<Row> rows;
+    for (int kb = 0; kb < p.nkb; ++kb) {
+        if (kb < nsplit) {
+            rows.push_back({(tiles(kb) + 1) / 2, kb, 0});
+            rows.push_back({tiles(kb) / 2, kb, 1});
+        } else {
+            rows.push_back({tiles(kb), kb, 0});
+        }
+    }
+    std::stable_sort(rows.begin(), rows.end(), [](const Row &x, const Row &y) { return x.cost > y.cost; });
+    for (size_t i = 0; i < rows.size(); ++i) p.slot[i] = static_cast<unsigned short>(2 * rows[i].kb + rows[i].part);
+    p.nsplit = nsplit;
+    return nsplit;
+}
+
 size_t bwd_ds_floats(int B, int H, int T) {
     const size_t nqt = (T + kBwdBQ - 1) / kBwdBQ;
     return static_cast<size_t>(B) * H * nqt * (nqt + 1) * kDsBlock;
@@ -683,7 +767,7 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
     }
     const dim3 block(256);
     const int rows = p.B * p.T * p.H;
-    const dim3 grid_d((rows + 15) / 16), grid_k(p.nkb * p.bh_pad), grid_q(p.nqb * p.bh_pad);
+    const dim3 grid_d((rows + 15) / 16), grid_k((p.nkb + p.nsplit) * p.bh_pad), grid_q(p.nqb * p.bh_pad);
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
     if (p.vec)
         attn_bwd_delta_kernel<true><<<grid_d, block, 0, stream>>>(p);

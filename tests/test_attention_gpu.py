@@ -249,6 +249,19 @@ def test_deterministic(rt):
         assert np.array_equal(u, w)
 
 
+def test_split_key_blocks_b1_t1024(rt, oracle):
+    """B*H = 12 heads of T = 1024 fill 96 of the GPU's dk/dv workgroup slots, so
+    each key block with two or more query tiles runs as two workgroups over
+    halves of its query range, adding into dK, dV rows the delta kernel zeroed:
+    oracle parity, and the same bits again (two addends in either order)."""
+    compare_with_oracle(rt, oracle, 1, 1024, 768, 12)
+    x, dy = qkv_inputs(rt, 1, 1024, 768, 31, 32)
+    a = run_layer(rt, x, dy, 12)
+    b = run_layer(rt, x, dy, 12)
+    for u, w in zip(a, b):
+        assert np.array_equal(u, w)
+
+
 def test_causality_at_full_length(rt):
     B, T, C, H = 2, 1024, 768, 12
     x, dy = qkv_inputs(rt, B, T, C, 21, 22)
