@@ -706,24 +706,34 @@ def attention_bench(args):
     # S and PV; dk/dv kernel dP, dV, dK; dq kernel dQ (delta does none).
     if k_ms:
         kernel_flops = {"fwd": 2 * unit, "bwd_delta": 0.0, "bwd_dkdv": 3 * unit, "bwd_dq": 1 * unit}
-        symbols = {"fwd": ("attn_fwd16_kernel", "attn_fwd_kernel"), "bwd_delta": ("attn_bwd_delta_kernel",),
-                   "bwd_dkdv": ("attn_bwd_dkdv_kernel",), "bwd_dq": ("attn_bwd_dq16_kernel", "attn_bwd_dq_kernel")}
+        # Kernel symbols per head size (D == 64: the 16-row kernels, and for
+        # short heads, T <= 128, the one-workgroup-per-block forward).
+        short = T <= 128
+        symbols = {"fwd": "attn_fwd_kernel" if D != 64 else ("attn_fwd_short_kernel" if short else "attn_fwd16_kernel"),
+                   "bwd_delta": "attn_bwd_delta_kernel", "bwd_dkdv": "attn_bwd_dkdv_kernel",
+                   "bwd_dq": "attn_bwd_dq16_kernel" if D == 64 else "attn_bwd_dq_kernel"}
         dom = "fwd" if fwd_only else max(k_ms, key=k_ms.get)
         if fwd_only:
-            achieved = fwd_bytes / (k_ms[dom] * 1e-3) / 1e9
+            # The forward is the only kernel of the timed region (K cold
+            # launches between two events): its average launch duration is
+            # the region over K, the same interval as `value`.
+            dur_ms, dur_src = ms_fwd_cold, "the timed region: K cold forward launches between two events, / K"
+            achieved = fwd_bytes / (dur_ms * 1e-3) / 1e9
             roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                     "algorithmic_bytes_per_launch": fwd_bytes}
         else:
-            achieved = kernel_flops[dom] / (k_ms[dom] * 1e-3) / 1e12
+            dur_ms, dur_src = k_ms[dom], "median of the per-kernel event pass"
+            achieved = kernel_flops[dom] / (dur_ms * 1e-3) / 1e12
             roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": round(peak, 2),
                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
                     "algorithmic_flop_per_launch": kernel_flops[dom]}
-        roof["duration_ms"] = round(k_ms[dom], 5)
+        roof["duration_ms"] = round(dur_ms, 5)
+        roof["duration_source"] = dur_src
         # HBM bytes per launch from the committed rocprof byte-counter runs
         # (FETCH_SIZE and WRITE_SIZE, scaled by a plain copy of known size).
         traffic_file = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.config}.json")
-        sym = symbols[dom][0] if D == 64 else symbols[dom][-1]
+        sym = symbols[dom]
         if os.path.exists(traffic_file):
             with open(traffic_file) as fh:
                 tr = json.load(fh)

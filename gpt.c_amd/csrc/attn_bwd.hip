@@ -10,8 +10,10 @@
 // using rowsum(dP o P) = rowsum(dO o O) =: delta.  These are the four
 // contractions of the reference; none is recomputed.
 //
-// Three kernels; every output element is written exactly once (no atomics,
-// no zeroed output needed, bit-for-bit deterministic):
+// Three kernels, bit-for-bit deterministic: every output element is written
+// once, except the dK, dV rows of a key block split in two (grids that leave
+// CUs idle, bwd_split_plan), which receive exactly two atomic adds into
+// rows zeroed by the delta kernel (a + b == b + a in fp32):
 //   attn_bwd_delta_kernel  delta = rowsum(dO o O); streams dO and O once.
 //   attn_bwd_dkdv_kernel   key-parallel: per 32-key wave (V resident in
 //                          registers), over the query tiles: P from P',

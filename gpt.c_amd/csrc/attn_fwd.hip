@@ -240,6 +240,83 @@ attn_fwd_kernel(const FwdParams a) {
     if (hf == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(l_tot)) * kLn2;
 }
 
+// ---- Per-tile math of the 16-row forwards ----
+//
+// One wave, 16 queries (lane (g, i16): query i16, keys 4g .. 4g+3 of each
+// 16-key block), one 64-key tile staged in LDS (rows of kLdsStride floats):
+// NKB of its 16-key blocks are visible (DIAG: the tile holding the block's
+// own keys, where block NKB - 1 is masked per key).
+//
+// Scores: S^T = K Q^T on 16 x 16 x 4 (Q^T in registers, qr[c][e] = Q[my_q]
+// [16g + 4c + e]), the tile's row maximum (log2 units), the online softmax
+// with lazy rescaling (the running maximum moves only when a row maximum
+// grows by more than 2^kRescaleLog2), P' = exp2(S c2 - m_use) into sc and its
+// row sums into l_run.  Returns m_use (0 while the row is all masked).
+template <int NKB, bool DIAG>
+__device__ __forceinline__ float fwd16_scores(const float *k_t, const f32x4 (&qr)[4], int g, int i16, float c2,
+                                              float &m_run, float &l_run, f32x4 (&acc)[4], f32x4 (&sc)[4]) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) sc[kb] = zero4();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        f32x4 ka[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+            ka[kb] = *reinterpret_cast<const f32x4 *>(&k_t[(16 * kb + i16) * kLdsStride + 16 * g + 4 * c]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) sc[kb] = mfma16(ka[kb][e], qr[c][e], sc[kb]);
+    }
+    if (DIAG) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (4 * g + r > i16) sc[NKB - 1][r] = -INFINITY;
+    }
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
+    const float mt = max4_rows(mx) * c2;
+
+    if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleLog2) != 0) {
+        const float m_new = fmaxf(m_run, mt);
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = fast_exp2(m_run - m_use);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+        m_run = m_new;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+    float ls[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float p = fast_exp2(fmaf(sc[kb][r], c2, -m_use));
+            sc[kb][r] = p;
+            ls[r & 1] += p;
+        }
+    l_run += ls[0] + ls[1];
+    return m_use;
+}
+
+// O^T += V^T P^T: step (kb, r) reduces keys 16kb + 4g' + r; lane i16's A
+// operands for the four dim blocks are V[key][4 i16 .. 4 i16 + 3] (one
+// 16-byte LDS read), and acc[db][r] = O[my_q][16g + 4r + db].
+template <int NKB>
+__device__ __forceinline__ void fwd16_pv(const float *v_t, const f32x4 (&sc)[4], int g, int i16, f32x4 (&acc)[4]) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const f32x4 va = *reinterpret_cast<const f32x4 *>(&v_t[(16 * kb + 4 * g + r) * kLdsStride + 4 * i16]);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] = mfma16(va[db], sc[kb][r], acc[db]);
+        }
+}
+
 // ---- The 16-row forward (D == 64, buffer-resource loads) ----
 //
 // One workgroup = 4 waves runs the 64-query blocks of its work list
@@ -349,54 +426,8 @@ attn_fwd16_kernel(const FwdParams a) {
     auto tile = [&](auto nkb_c, auto diag_c) {
         constexpr int NKB = decltype(nkb_c)::value;
         constexpr bool DIAG = decltype(diag_c)::value;
-
-        f32x4 sc[4];  // S^T: sc[kb][r] = S[my_q][16kb + 4g + r]
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) sc[kb] = zero4();
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            f32x4 ka[NKB];
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
-                ka[kb] = *reinterpret_cast<const f32x4 *>(&k_lds[(16 * kb + i16) * kLdsStride + 16 * g + 4 * c]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb) sc[kb] = mfma16(ka[kb][e], qr[c][e], sc[kb]);
-        }
-        if (DIAG) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (4 * g + r > i16) sc[NKB - 1][r] = -INFINITY;
-        }
-
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-            mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
-        const float mt = max4_rows(mx) * c2;
-
-        // Lazy rescaling, as in the kernel above.
-        if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleLog2) != 0) {
-            const float m_new = fmaxf(m_run, mt);
-            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-            const float alpha = fast_exp2(m_run - m_use);
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-            m_run = m_new;
-        }
-        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
-        float ls[2] = {0.0f, 0.0f};
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float p = fast_exp2(fmaf(sc[kb][r], c2, -m_use));
-                sc[kb][r] = p;
-                ls[r & 1] += p;
-            }
-        l_run += ls[0] + ls[1];
+        f32x4 sc[4];
+        const float m_use = fwd16_scores<NKB, DIAG>(k_lds, qr, g, i16, c2, m_run, l_run, acc, sc);
 
         // P' rows of block (jq, key blocks 2kt and 2kt + 1), zeros past the
         // diagonal; m of this tile (not for short heads, whose backward
@@ -410,17 +441,7 @@ attn_fwd16_kernel(const FwdParams a) {
                     kb < NKB ? sc[kb] : zero4();
             if (g == 0 && my_q < T) a.pm[(static_cast<uint32_t>(bh) * nqt + kt) * T + my_q] = m_use;
         }
-
-        // O^T += V^T P^T: step (kb, r) reduces keys 16kb + 4g' + r; lane i's
-        // A operands for the four dim blocks are V[key][4i .. 4i+3].
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const f32x4 va = *reinterpret_cast<const f32x4 *>(&v_lds[(16 * kb + 4 * g + r) * kLdsStride + 4 * i16]);
-#pragma unroll
-                for (int db = 0; db < 4; ++db) acc[db] = mfma16(va[db], sc[kb][r], acc[db]);
-            }
+        fwd16_pv<NKB>(v_lds, sc, g, i16, acc);
     };
 
     for (;;) {
@@ -527,13 +548,127 @@ attn_fwd16_kernel(const FwdParams a) {
     }
 }
 
+// ---- Short heads (T <= 128, D == 64, compact layout) ----
+//
+// One workgroup per 64-query block (at most two key tiles), the blocks with
+// two tiles first; the (head, block) pair comes from blockIdx alone, so the
+// first loads issue without waiting for a work list.  Q, every key tile of
+// the block and the bias go out at once; both K/V tiles are staged behind
+// one barrier, and the waves then run the tiles back to back (the same
+// per-tile math as the kernel above).  The backward of short heads
+// recomputes P, so no P' or m is stored.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_fwd_short_kernel(const FwdParams a) {
+    constexpr int TILE = kFwdBN * kLdsStride;
+    __shared__ __attribute__((aligned(16))) float k_lds[kShortHeadTiles * TILE];
+    __shared__ __attribute__((aligned(16))) float v_lds[kShortHeadTiles * TILE];
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
+    const int BH = a.B * a.H, T = a.T;
+    const int r = static_cast<int>(blockIdx.x) / BH;
+    const int bh = static_cast<int>(blockIdx.x) - r * BH;
+    const int jq = a.nqt - 1 - r;  // grid = BH * nqt, so 0 <= jq < nqt
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int my_q = jq * kF16Rows + 16 * w + i16;
+
+    // Rows past T read as zeros (buffer resources over the head's T rows).
+    const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
+    const auto k_rows = head_rows(a.k.p + b * a.k.sb + h * a.k.sh, T, a.k.st);
+    const auto v_rows = head_rows(a.v.p + b * a.v.sb + h * a.v.sh, T, a.v.st);
+    f32x4 qr[4];  // Q[my_q][16g + 4c + e] in qr[c][e]
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(my_q) * a.q.st + 16 * g + 4 * c);
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    f32x4 kpre[kShortHeadTiles][4], vpre[kShortHeadTiles][4];
+#pragma unroll
+    for (int kt = 0; kt < kShortHeadTiles; ++kt)
+        if (kt <= jq) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t key = kt * kFwdBN + ld_row + 16 * i;
+                kpre[kt][i] = buffer_load4(k_rows, key * a.k.st + ld_col);
+                vpre[kt][i] = buffer_load4(v_rows, key * a.v.st + ld_col);
+            }
+        }
+    // The qkv Linear's bias, read by every thread for its own columns.  Key
+    // rows past T then hold the bias: they only occur past the diagonal of
+    // every query < T (masked), and rows of queries past T are not written.
+    const bool biased = a.kb != nullptr;
+    f32x4 kb4 = zero4(), vb4 = zero4(), qb4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qb4[c] = zero4();
+    if (biased) {
+        kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + ld_col);
+        vb4 = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + ld_col);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qb4[c] = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * g + 4 * c);
+    }
+#pragma unroll
+    for (int kt = 0; kt < kShortHeadTiles; ++kt)
+        if (kt <= jq) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = ld_row + 16 * i;
+                *reinterpret_cast<f32x4 *>(&k_lds[kt * TILE + row * kLdsStride + ld_col]) = kpre[kt][i] + kb4;
+                *reinterpret_cast<f32x4 *>(&v_lds[kt * TILE + row * kLdsStride + ld_col]) = vpre[kt][i] + vb4;
+            }
+        }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qr[c] += qb4[c];
+    __syncthreads();
+
+    const float c2 = a.scale_log2;
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4 acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = zero4();
+    f32x4 sc[4];
+    if (jq > 0) {  // a full tile before the diagonal one (kShortHeadTiles == 2)
+        fwd16_scores<4, false>(k_lds, qr, g, i16, c2, m_run, l_run, acc, sc);
+        fwd16_pv<4>(v_lds, sc, g, i16, acc);
+    }
+    const float *k_d = k_lds + jq * TILE, *v_d = v_lds + jq * TILE;
+    switch (w) {  // wave-uniform: the 16-key blocks of the diagonal tile this wave sees
+        case 0: fwd16_scores<1, true>(k_d, qr, g, i16, c2, m_run, l_run, acc, sc); fwd16_pv<1>(v_d, sc, g, i16, acc); break;
+        case 1: fwd16_scores<2, true>(k_d, qr, g, i16, c2, m_run, l_run, acc, sc); fwd16_pv<2>(v_d, sc, g, i16, acc); break;
+        case 2: fwd16_scores<3, true>(k_d, qr, g, i16, c2, m_run, l_run, acc, sc); fwd16_pv<3>(v_d, sc, g, i16, acc); break;
+        default: fwd16_scores<4, true>(k_d, qr, g, i16, c2, m_run, l_run, acc, sc); fwd16_pv<4>(v_d, sc, g, i16, acc); break;
+    }
+
+    // y = O / l and the log-sum-exp.
+    const float lt = sum4_rows(l_run);
+    if (my_q < T) {
+        const float inv = 1.0f / lt;
+        float *orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g;
+        float *o2row = a.o2 ? a.o2 + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g : nullptr;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const f32x4 val = {acc[0][rr] * inv, acc[1][rr] * inv, acc[2][rr] * inv, acc[3][rr] * inv};
+            *reinterpret_cast<f32x4 *>(orow + 4 * rr) = val;
+            if (o2row) *reinterpret_cast<f32x4 *>(o2row + 4 * rr) = val;
+        }
+        if (g == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (m_run + log2f(lt)) * kLn2;
+    }
+}
+
 void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     FwdParams p = p_in;
     const bool perm = p.qp != nullptr;
     if (p.full) {
-        // Short heads take the DEEP variant and leave P' to the backward.
+        // Short heads leave P' to the backward; in the compact layout they
+        // run one workgroup per block, in the reference layout the DEEP
+        // variant of the work-list kernel (which also writes the caches).
         const bool deep = p.nqt <= kShortHeadTiles;
         if (deep) p.pp = p.pm = nullptr;
+        if (deep && !perm) {
+            if (ev) hipCheck(hipEventRecord(ev[0], stream));
+            attn_fwd_short_kernel<<<dim3(p.B * p.H * p.nqt), dim3(256), 0, stream>>>(p);
+            hipCheck(hipGetLastError());
+            if (ev) hipCheck(hipEventRecord(ev[1], stream));
+            return;
+        }
         const void *kern = deep ? (perm ? reinterpret_cast<const void *>(attn_fwd16_kernel<true, true>)
                                         : reinterpret_cast<const void *>(attn_fwd16_kernel<false, true>))
                                 : (perm ? reinterpret_cast<const void *>(attn_fwd16_kernel<true, false>)
