@@ -706,10 +706,10 @@ def attention_bench(args):
     # S and PV; dk/dv kernel dP, dV, dK; dq kernel dQ (delta does none).
     if k_ms:
         kernel_flops = {"fwd": 2 * unit, "bwd_delta": 0.0, "bwd_dkdv": 3 * unit, "bwd_dq": 1 * unit}
-        # Kernel symbols per head size (D == 64: the 16-row kernels, and for
-        # short heads, T <= 128, the one-workgroup-per-block forward).
-        short = T <= 128
-        symbols = {"fwd": "attn_fwd_kernel" if D != 64 else ("attn_fwd_short_kernel" if short else "attn_fwd16_kernel"),
+        # Kernel symbols per head size (D == 64: the 16-row kernels; short
+        # heads: T <= 64 one workgroup per block, 64 < T <= 128 two per head).
+        fwd_sym = "attn_fwd16_kernel" if T > 128 else ("attn_fwd_twotile_kernel" if T > 64 else "attn_fwd_short_kernel")
+        symbols = {"fwd": "attn_fwd_kernel" if D != 64 else fwd_sym,
                    "bwd_delta": "attn_bwd_delta_kernel", "bwd_dkdv": "attn_bwd_dkdv_kernel",
                    "bwd_dq": "attn_bwd_dq16_kernel" if D == 64 else "attn_bwd_dq_kernel"}
         dom = "fwd" if fwd_only else max(k_ms, key=k_ms.get)

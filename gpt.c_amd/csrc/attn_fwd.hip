@@ -671,6 +671,184 @@ attn_fwd_short_kernel(const FwdParams a) {
     }
 }
 
+// ---- Two-tile heads (64 < T <= 128, D == 64, compact layout) ----
+//
+// A head of two 64-query blocks is 36 units of MFMA work, a unit being one
+// 16-query slab against one 16-key block: the second block's four slabs
+// see 4 + 1, 4 + 2, 4 + 3 and 4 + 4 units (its full first tile, then its
+// diagonal tile), the first block's 1, 2, 3 and 4.  With one workgroup per
+// block (the kernel above) the last wave of the second block carries 8 in a
+// row, one wave per SIMD.  Here two workgroups per head share the 36 units
+// so that no wave carries more than 5; a slab whose two tiles run on two
+// waves has its partial softmax state (running max, sums, O) merged through
+// LDS after the workgroup's one barrier of the compute phase:
+//   role 0: w0 slab (1,3) tile 0 -> partial 0; w1 slab (1,3) diagonal, merges 0;
+//           w2 slab (1,0) both tiles; w3 slabs (0,3) and (0,0)
+//   role 1: w0 slab (1,1) tile 0 -> partial 0; w1 slab (1,2) tile 0 -> partial 1;
+//           w2 slab (0,1), then (1,2) diagonal, merges 1;
+//           w3 slab (0,2), then (1,1) diagonal, merges 0
+// (slab (j, s): queries 64j + 16s .. 64j + 16s + 15).  Both workgroups stage
+// the head's two K/V tiles.
+struct SlabState {
+    float m_run, l_run;
+    f32x4 acc[4];
+};
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+attn_fwd_twotile_kernel(const FwdParams a) {
+    constexpr int TILE = kFwdBN * kLdsStride;
+    __shared__ __attribute__((aligned(16))) float k_lds[2 * TILE];
+    __shared__ __attribute__((aligned(16))) float v_lds[2 * TILE];
+    __shared__ __attribute__((aligned(16))) f32x4 part_lds[2][5][64];  // [partial][acc0..3, {m, l}][lane]
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
+    const int BH = a.B * a.H, T = a.T;
+    const int role = static_cast<int>(blockIdx.x) / BH;  // grid = 2 * BH
+    const int bh = static_cast<int>(blockIdx.x) - role * BH;
+    const int b = bh / a.H, h = bh - b * a.H;
+
+    const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
+    const auto k_rows = head_rows(a.k.p + b * a.k.sb + h * a.k.sh, T, a.k.st);
+    const auto v_rows = head_rows(a.v.p + b * a.v.sb + h * a.v.sh, T, a.v.st);
+    // This wave's slabs (first, second): (block j, slab s) as listed above.
+    const int job = 4 * role + w;  // wave-uniform
+    constexpr int kJobSlabs[8][4] = {{1, 3, -1, 0}, {1, 3, -1, 0}, {1, 0, -1, 0}, {0, 3, 0, 0},
+                                     {1, 1, -1, 0}, {1, 2, -1, 0}, {0, 1, 1, 2}, {0, 2, 1, 1}};
+    // The Q rows of the wave's slabs (loaded after the K/V staging: issuing
+    // them first measured no faster, warm or cold).
+    f32x4 qa[4], qb[4];
+    auto load_q = [&](int j, int sl, f32x4(&qr)[4]) {
+        const int q = j * kF16Rows + 16 * sl + i16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c);
+    };
+    const bool two_slabs = kJobSlabs[job][2] >= 0;
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    f32x4 kpre[2][4], vpre[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t key = kt * kFwdBN + ld_row + 16 * i;
+            kpre[kt][i] = buffer_load4(k_rows, key * a.k.st + ld_col);
+            vpre[kt][i] = buffer_load4(v_rows, key * a.v.st + ld_col);
+        }
+    // The qkv bias: key rows past T then hold the bias; they are masked for
+    // every query < T, and rows of queries past T are not written.
+    const bool biased = a.kb != nullptr;
+    f32x4 kb4 = zero4(), vb4 = zero4(), qb4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qb4[c] = zero4();
+    if (biased) {
+        kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + ld_col);
+        vb4 = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + ld_col);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qb4[c] = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * g + 4 * c);
+    }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ld_row + 16 * i;
+            *reinterpret_cast<f32x4 *>(&k_lds[kt * TILE + row * kLdsStride + ld_col]) = kpre[kt][i] + kb4;
+            *reinterpret_cast<f32x4 *>(&v_lds[kt * TILE + row * kLdsStride + ld_col]) = vpre[kt][i] + vb4;
+        }
+    __syncthreads();
+
+    const float c2 = a.scale_log2;
+    f32x4 qr[4];
+    // Q of the wave's first (second) slab, with the q bias.
+    auto use_q = [&](const f32x4(&src)[4]) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qr[c] = src[c] + qb4[c];
+    };
+    auto fresh = [](SlabState &st) {
+        st.m_run = -INFINITY;
+        st.l_run = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) st.acc[db] = zero4();
+    };
+    f32x4 sc[4];
+    auto full_tile0 = [&](SlabState &st) {
+        fwd16_scores<4, false>(k_lds, qr, g, i16, c2, st.m_run, st.l_run, st.acc, sc);
+        fwd16_pv<4>(v_lds, sc, g, i16, st.acc);
+    };
+    // Slab s of block j against its diagonal tile j: key blocks 0 .. s, the last masked per key.
+    auto diag = [&](auto s_c, int j, SlabState &st) {
+        constexpr int NKB = decltype(s_c)::value + 1;
+        fwd16_scores<NKB, true>(k_lds + j * TILE, qr, g, i16, c2, st.m_run, st.l_run, st.acc, sc);
+        fwd16_pv<NKB>(v_lds + j * TILE, sc, g, i16, st.acc);
+    };
+    auto finish = [&](int j, int sl, const SlabState &st) {
+        const int my_q = j * kF16Rows + 16 * sl + i16;
+        const float lt = sum4_rows(st.l_run);
+        if (my_q < T) {
+            const float inv = 1.0f / lt;
+            float *orow = a.o.p + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g;
+            float *o2row = a.o2 ? a.o2 + b * a.o.sb + my_q * a.o.st + h * a.o.sh + 16 * g : nullptr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const f32x4 val = {st.acc[0][r] * inv, st.acc[1][r] * inv, st.acc[2][r] * inv, st.acc[3][r] * inv};
+                *reinterpret_cast<f32x4 *>(orow + 4 * r) = val;
+                if (o2row) *reinterpret_cast<f32x4 *>(o2row + 4 * r) = val;
+            }
+            if (g == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (st.m_run + log2f(lt)) * kLn2;
+        }
+    };
+    auto put_partial = [&](int slot, const SlabState &st) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) part_lds[slot][db][lane] = st.acc[db];
+        part_lds[slot][4][lane] = f32x4{st.m_run, st.l_run, 0.0f, 0.0f};
+    };
+    // st (the diagonal tile) merged with partial `slot` (the full tile 0):
+    // both running maxima are finite (every query sees key 0 and its own key).
+    auto merge = [&](int slot, SlabState &st) {
+        const f32x4 ml = part_lds[slot][4][lane];
+        const float m = fmaxf(st.m_run, ml[0]);
+        const float fa = fast_exp2(st.m_run - m), fb = fast_exp2(ml[0] - m);
+        st.l_run = st.l_run * fa + ml[1] * fb;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) st.acc[db] = st.acc[db] * fa + part_lds[slot][db][lane] * fb;
+        st.m_run = m;
+    };
+
+    load_q(kJobSlabs[job][0], kJobSlabs[job][1], qa);
+    if (two_slabs) load_q(kJobSlabs[job][2], kJobSlabs[job][3], qb);
+    SlabState st;
+    fresh(st);
+    use_q(qa);
+    // Compute phase: at most 5 units per wave.
+    switch (job) {
+        case 0: full_tile0(st); put_partial(0, st); break;
+        case 1: diag(IntC<3>{}, 1, st); break;
+        case 2: full_tile0(st); diag(IntC<0>{}, 1, st); finish(1, 0, st); break;
+        case 3:
+            diag(IntC<3>{}, 0, st); finish(0, 3, st);
+            fresh(st); use_q(qb); diag(IntC<0>{}, 0, st); finish(0, 0, st);
+            break;
+        case 4: full_tile0(st); put_partial(0, st); break;
+        case 5: full_tile0(st); put_partial(1, st); break;
+        case 6:
+            diag(IntC<1>{}, 0, st); finish(0, 1, st);
+            fresh(st); use_q(qb); diag(IntC<2>{}, 1, st);
+            break;
+        default:
+            diag(IntC<2>{}, 0, st); finish(0, 2, st);
+            fresh(st); use_q(qb); diag(IntC<1>{}, 1, st);
+            break;
+    }
+    __syncthreads();
+    // Merge phase.
+    switch (job) {
+        case 1: merge(0, st); finish(1, 3, st); break;
+        case 6: merge(1, st); finish(1, 2, st); break;
+        case 7: merge(0, st); finish(1, 1, st); break;
+        default: break;
+    }
+}
+
 void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     FwdParams p = p_in;
     const bool perm = p.qp != nullptr;
@@ -682,7 +860,10 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
         if (deep) p.pp = p.pm = nullptr;
         if (deep && !perm) {
             if (ev) hipCheck(hipEventRecord(ev[0], stream));
-            attn_fwd_short_kernel<<<dim3(p.B * p.H * p.nqt), dim3(256), 0, stream>>>(p);
+            if (p.nqt == 2)
+                attn_fwd_twotile_kernel<<<dim3(2 * p.B * p.H), dim3(256), 0, stream>>>(p);
+            else
+                attn_fwd_short_kernel<<<dim3(p.B * p.H * p.nqt), dim3(256), 0, stream>>>(p);
             hipCheck(hipGetLastError());
             if (ev) hipCheck(hipEventRecord(ev[1], stream));
             return;
