@@ -96,6 +96,8 @@ SMALL = [  # (B, T, C, H)
     (2, 77, 384, 4),       # D = 96 (kernels built for 128 padded dims)
     (1, 200, 768, 6),      # D = 128
     (2, 33, 260, 4),       # D = 65 (128 padded dims, ragged)
+    (3, 65, 128, 2),       # two-tile head: one query in the second block
+    (1, 127, 192, 3),      # two-tile head, ragged second block
 ]
 
 
@@ -260,6 +262,12 @@ def test_split_key_blocks_b1_t1024(rt, oracle):
     b = run_layer(rt, x, dy, 12)
     for u, w in zip(a, b):
         assert np.array_equal(u, w)
+
+
+def test_split_key_blocks_ragged_t(rt, oracle):
+    """Split key blocks when T is not a multiple of the 64-query tile (T = 1000:
+    the last key block and the last query half are partial)."""
+    compare_with_oracle(rt, oracle, 1, 1000, 768, 12)
 
 
 def test_causality_at_full_length(rt):

@@ -135,6 +135,7 @@ def test_gpt2_training_steps_match_oracle(rt, oracle, V, block, L, H, C, B, T):
     (1, 300, 128, 2),   # ragged T, folded
     (2, 77, 96, 4),     # D = 24: the bias is added to the qkv activations instead
     (2, 64, 256, 2),    # D = 128 (the 128-dim kernels), bias added to the activations
+    (3, 65, 128, 2),    # two-tile heads with the bias folded into the short-head kernels
 ])
 def test_self_attention_block_matches_oracle(rt, oracle, B, T, C, H):
     """SelfAttention (self_attention.c:47-83): forward and backward through
