@@ -3,6 +3,7 @@
 // Replaces kernels/src/cuda/Attention.cu:170-324 behind the signatures of
 // kernels/src/cuda/Attention.h:9-22 (called by
 // kernels/src/core/Attention.c:40-41,75-76).
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <initializer_list>
@@ -78,11 +79,13 @@ int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 //   db partials (B*nqt*C + B*2nkb*2C)       column sums of the dq | dk, dv
 //                                            rows (qkv bias folded in only)
 //   P' / dS blocks (bwd_ds_floats)           P' from forward, dS in backward
+// The LSE-only state (lse_only) has no m and no P' / dS blocks: its
+// backward recomputes P from the log-sum-exp in both gradient kernels.
 struct StateLayout {
     int64_t y, lse, delta, m, dbq, dbkv, p, total;
 };
 
-StateLayout state_layout(const Dims &d, bool reference_layout) {
+StateLayout state_layout(const Dims &d, bool reference_layout, bool lse_only) {
     const int64_t btc = static_cast<int64_t>(d.B) * d.T * d.C;
     const int64_t bht = static_cast<int64_t>(d.B) * d.H * d.T;
     const int64_t nqt = (d.T + 63) / 64;
@@ -97,17 +100,31 @@ StateLayout state_layout(const Dims &d, bool reference_layout) {
     s.delta = off;
     off += align64(bht);
     s.m = off;
-    off += align64(bht * nqt);
+    if (!lse_only) off += align64(bht * nqt);
     const int64_t nkb = (d.T + 127) / 128;
     s.dbq = off;
     off += align64(static_cast<int64_t>(d.B) * nqt * d.C);
     s.dbkv = off;  // up to 2 nkb rows per batch row: split key blocks add one each
     off += align64(static_cast<int64_t>(d.B) * 2 * nkb * 2 * d.C);
     s.p = off;
-    off += static_cast<int64_t>(gptc::bwd_ds_floats(d.B, d.H, d.T));
+    if (!lse_only) off += static_cast<int64_t>(gptc::bwd_ds_floats(d.B, d.H, d.T));
     s.total = off;
+    return s;
+}
+
+// Largest P' state (floats) a forward keeps; above it, kernels that can
+// (D == 64 with 16-byte rows) keep the LSE-only state instead.  The default
+// is the int length of a tensor_t, past which the state cannot exist.
+std::atomic<long long> g_state_limit{INT32_MAX};
+
+// The state layout a forward uses: LSE-only when the D == 64 kernels run
+// (`full`) and the P' state would exceed the limit.
+StateLayout forward_state(const Dims &d, bool reference_layout, bool full, bool *lse_only) {
+    *lse_only = full && state_layout(d, reference_layout, false).total > g_state_limit.load();
+    const StateLayout s = state_layout(d, reference_layout, *lse_only);
     CHECK_ERROR(s.total > INT32_MAX,
-                "Attention state of %lld floats for B=%d, T=%d, H=%d exceeds the int length of a tensor_t.",
+                "Attention state of %lld floats for B=%d, T=%d, H=%d exceeds the int length of a tensor_t "
+                "(head sizes other than 64 keep the probability blocks).",
                 (long long)s.total, d.B, d.T, d.H);
     return s;
 }
@@ -181,7 +198,22 @@ void forward_impl(const tensor_t *input, const tensor_t *bias, const tensor_t *m
     const int64_t bht = static_cast<int64_t>(d.B) * d.H * d.T;
 
     const bool compact = cache[0] == input || cache[0]->t == input->t;
-    const StateLayout st = state_layout(d, !compact);
+    // Whether the D == 64 kernels run (they decide which state is kept): the
+    // views' alignment, y's second copy (a buffer of its own in the compact
+    // layout; in the reference layout it lies in the state, 256-byte aligned)
+    // and the permuted caches of the reference layout.
+    p.B = d.B;
+    p.H = d.H;
+    p.T = d.T;
+    p.D = d.D;
+    {
+        const float *o2 = compact ? (cache[1]->t == output->t ? nullptr : cache[1]->t) : nullptr;
+        p.vec = (d.D % 4 == 0) && aligned16(input->t) && aligned16(output->t) && aligned16(o2) &&
+                (compact || (aligned16(cache[0]->t) && aligned16(cache[1]->t) && aligned16(cache[2]->t)));
+        p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.v.st});
+    }
+    bool lse_only = false;
+    const StateLayout st = forward_state(d, !compact, p.full, &lse_only);
     if (compact) {
         // Compact layout: the layer keeps the input itself, y in cache[1]
         // (the output's own storage, or a buffer that receives a copy), the
@@ -208,20 +240,13 @@ void forward_impl(const tensor_t *input, const tensor_t *bias, const tensor_t *m
         p.kp = cache[1]->t;
         p.vp = cache[2]->t;
     }
-    p.pm = cache[3]->t + st.m;
-    p.pp = cache[3]->t + st.p;
+    p.pm = lse_only ? nullptr : cache[3]->t + st.m;
+    p.pp = lse_only ? nullptr : cache[3]->t + st.p;
 
-    p.B = d.B;
-    p.H = d.H;
-    p.T = d.T;
-    p.D = d.D;
     p.scale_log2 = gptc::kLog2e / std::sqrt(static_cast<float>(d.D));
     p.nqb = (d.T + 127) / 128;
     p.nqt = (d.T + 63) / 64;
     p.bh_pad = bh_padded(d.B * d.H);
-    p.vec = (d.D % 4 == 0) && aligned16(input->t) && aligned16(output->t) && aligned16(p.o2) &&
-            (!p.qp || (aligned16(p.qp) && aligned16(p.kp) && aligned16(p.vp)));
-    p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.v.st});
     if (bias != nullptr) {
         CHECK_ERROR(!compact, "The qkv bias can be folded in with the compact cache layout only.");
         CHECK_ERROR(bias->device != CUDA || bias->length != 3 * d.C, "Expected a GPU bias of 3C = %d elements.",
@@ -288,7 +313,11 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
     const tensor_t *c0 = cache[0];
     const float *y_saved = nullptr;
     const bool compact = c0->ndims == 3 && c0->shape[0] == d.B && c0->shape[1] == d.T && c0->shape[2] == 3 * d.C;
-    const StateLayout st = state_layout(d, !compact);
+    // Which state the forward kept: told apart by its length (the LSE-only
+    // state has no probability blocks, so it is strictly shorter).
+    const StateLayout st_lse = state_layout(d, !compact, true);
+    const bool lse_only = cache[3]->ndims == 1 && cache[3]->length == st_lse.total;
+    const StateLayout st = lse_only ? st_lse : state_layout(d, !compact, false);
     CHECK_ERROR(cache[3]->ndims != 1 || cache[3]->length != st.total,
                 "cache[3] does not hold the state written by attention_forward_cuda_kernel for this shape.");
     if (compact) {
@@ -309,10 +338,11 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
     }
     p.o = btc_view<HeadView>(y_saved, d);
     p.delta = cache[3]->t + st.delta;
-    p.pm = cache[3]->t + st.m;
     // The backward consumes the state: dS overwrites P' (gpt.c's CPU backward
     // likewise reuses its caches as scratch, kernels/src/cpu/Attention.c:198-201).
-    p.ds = cache[3]->t + st.p;
+    // The LSE-only state has neither: both gradient kernels recompute P.
+    p.pm = lse_only ? nullptr : cache[3]->t + st.m;
+    p.ds = lse_only ? nullptr : cache[3]->t + st.p;
     p.dout = btc_view<HeadView>(static_cast<const float *>(global_grad->t), d);
     const uint32_t sb3 = static_cast<uint32_t>(d.T) * 3 * d.C, st3 = 3 * d.C;
     p.dq = HeadViewW{dout->t, sb3, st3, static_cast<uint32_t>(d.D)};
@@ -331,6 +361,9 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
     p.vec = (d.D % 4 == 0) && aligned16(p.q.p) && aligned16(p.k.p) && aligned16(p.v.p) && aligned16(y_saved) &&
             aligned16(global_grad->t) && aligned16(dout->t);
     p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.dout.st});
+    CHECK_ERROR(lse_only && !p.full,
+                "The forward kept the log-sum-exp-only state, which only the D = 64 kernels read, but these "
+                "gradient buffers need the other kernels (unaligned rows).");
     hipStream_t s = gptc_stream_checked();
     gptc::bwd_split_plan(p);
     bool folded = false;
@@ -387,7 +420,15 @@ extern "C" long long gptc_attention_state_floats(int B, int T, int C, int n_head
                 "Expected B, T, C >= 0 and C divisible by n_heads > 0, but got B=%d, T=%d, C=%d, n_heads=%d.", B, T,
                 C, n_heads);
     const Dims d{B, T, C, n_heads, C / n_heads};
-    return state_layout(d, false).total;
+    // The state the forward keeps in the compact layout, taking head size 64
+    // to run the D == 64 kernels (a forward that finds otherwise re-points
+    // cache[3] to its own size).
+    bool lse_only = false;
+    return forward_state(d, false, d.D == gptc::kDPad, &lse_only).total;
+}
+
+extern "C" long long gptc_attention_set_state_limit(long long floats) {
+    return g_state_limit.exchange(floats < 0 ? static_cast<long long>(INT32_MAX) : floats);
 }
 
 namespace {

@@ -334,10 +334,13 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
                 for (int c = 0; c < 4; ++c) dp[4 * g + c] = s[4 * g + c] * (dp[4 * g + c] - d4[c]);  // dS
             }
 
-            // dS replaces P' in place: block (qt, key block kw0/32), [64 queries][32 keys].
-            float *hb = half_base(qt, qb);
+            // dS replaces P' in place: block (qt, key block kw0/32), [64 queries][32 keys]
+            // (none with the LSE-only state, whose dq kernel recomputes it).
+            if (!RECOMP || a.ds != nullptr) {
+                float *hb = half_base(qt, qb);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
+                for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
+            }
 
             // dV += P^T dO and dK += dS^T Q (keys x dims).
 #pragma unroll
@@ -687,6 +690,212 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
     }
 }
 
+// ---- dQ recomputing P and dP (the LSE-only backward, D == 64) ----
+//
+// For a forward that stored no P' (its state would not fit, or the caller
+// capped it): the dk/dv kernel recomputes P and writes no dS, and this
+// kernel forms dQ from the saved statistics alone.  It runs the forward's
+// work lists (block_sched.hpp) with its tile layout: a workgroup is 4 waves
+// x 16 queries of a 64-query block, K and V tiles of 64 keys are staged in
+// LDS (prefetched one step ahead), and lane (g, i16) owns query i16 of the
+// wave and keys 4g .. 4g+3 of each 16-key block.  Per tile:
+//   S^T = K Q^T and dP^T = V dO^T (Q and dO rows in registers as B operands),
+//   P = exp2(S log2(e)/sqrt(D) - LSE log2(e)), zero above the diagonal,
+//   dS = P o (dP - delta),  dQ^T += K^T dS^T  (K rows as A operands, dS^T
+//   straight from the accumulators, as O^T += V^T P^T in the forward).
+// Three contractions per tile where the dq16 kernel reads dS and does one.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_bwd_dq16_recomp_kernel(const BwdParams a) {
+    constexpr int LS = kLdsStride;
+    __shared__ __attribute__((aligned(16))) float k_lds[kBwdBQ * LS];
+    __shared__ __attribute__((aligned(16))) float v_lds[kBwdBQ * LS];
+    __shared__ float red_lds[4][kDPad];  // db column sums of the block's dQ rows, per wave
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
+    const int it_end = a.sched.wg_start[blockIdx.x + 1];
+    int it = a.sched.wg_start[blockIdx.x];
+    if (it >= it_end) return;
+    const int T = a.T;
+    const float c2 = a.scale * kLog2e;
+
+    auto advance = [&](int &sit, int &skt, int &sbh, int &sj) {
+        if (skt < sj) {
+            ++skt;
+            return true;
+        }
+        if (++sit >= it_end) return false;
+        const int item = a.sched.items[sit];
+        sbh = sched_bh(item);
+        sj = sched_j(item);
+        skt = 0;
+        return true;
+    };
+
+    // Cooperative K/V tile load: thread covers rows (tid >> 4) + 16i, dims
+    // 4 (tid & 15); rows past T read as zeros.  With the qkv bias folded in,
+    // each thread adds the k and v bias of its dims as it stores the tile.
+    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
+    const bool biased = a.kb != nullptr;
+    f32x4 kpre[4], vpre[4], kb4 = zero4(), vb4 = zero4();
+    auto load_tile = [&](int hbh, int kt) {
+        const int hb = hbh / a.H, hh = hbh - hb * a.H;
+        const auto k_rows = head_rows(a.k.p + hb * a.k.sb + hh * a.k.sh, T, a.k.st);
+        const auto v_rows = head_rows(a.v.p + hb * a.v.sb + hh * a.v.sh, T, a.v.st);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t key = kt * kBwdBQ + ld_row + 16 * i;
+            kpre[i] = buffer_load4(k_rows, key * a.k.st + ld_col);
+            vpre[i] = buffer_load4(v_rows, key * a.v.st + ld_col);
+        }
+        if (biased) {
+            kb4 = *reinterpret_cast<const f32x4 *>(a.kb + hh * kDPad + ld_col);
+            vb4 = *reinterpret_cast<const f32x4 *>(a.vb + hh * kDPad + ld_col);
+        }
+    };
+
+    int kt = 0, bh = sched_bh(a.sched.items[it]), jq = sched_j(a.sched.items[it]);
+    // The wave's rows of the current block: Q (with its bias) and dO as B
+    // operands (qr[c][e] = Q[my_q][16g + 4c + e]), and the query's LSE log2(e)
+    // and delta (rows past T read a clamped row and are never stored).
+    f32x4 qr[4], dor[4];
+    float lse2 = 0.0f, dl = 0.0f;
+    int my_q = 0;
+    auto load_rows = [&]() {
+        const int b = bh / a.H, h = bh - b * a.H;
+        my_q = jq * kBwdBQ + 16 * w + i16;
+        const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
+        const auto d_rows = head_rows(a.dout.p + b * a.dout.sb + h * a.dout.sh, T, a.dout.st);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(my_q) * a.q.st + 16 * g + 4 * c);
+            dor[c] = buffer_load4(d_rows, static_cast<uint32_t>(my_q) * a.dout.st + 16 * g + 4 * c);
+            if (biased) qr[c] += *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * g + 4 * c);
+        }
+        const int qc = min(my_q, T - 1);
+        lse2 = a.lse[static_cast<uint32_t>(bh) * T + qc] * kLog2e;
+        dl = a.delta[static_cast<uint32_t>(bh) * T + qc];
+    };
+    load_rows();
+    load_tile(bh, 0);
+    int pit = it, pkt = 0, pbh = bh, pj = jq;  // the step whose tile is loaded next
+    bool pre_ok = advance(pit, pkt, pbh, pj);
+
+    f32x4 acc[4];  // dQ^T: acc[db][r] = dQ[my_q][16g + 4r + db] before the 1/sqrt(D) scaling
+    // One key tile: NKB 16-key blocks visible to the wave's queries (DIAG:
+    // the block's own tile, block NKB - 1 masked per key).
+    auto tile = [&](auto nkb_c, auto diag_c) {
+        constexpr int NKB = decltype(nkb_c)::value;
+        constexpr bool DIAG = decltype(diag_c)::value;
+        f32x4 sc[4], dp[4];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) sc[kb] = dp[kb] = zero4();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            f32x4 ka[NKB], va[NKB];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                ka[kb] = *reinterpret_cast<const f32x4 *>(&k_lds[(16 * kb + i16) * LS + 16 * g + 4 * c]);
+                va[kb] = *reinterpret_cast<const f32x4 *>(&v_lds[(16 * kb + i16) * LS + 16 * g + 4 * c]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    sc[kb] = mfma16(ka[kb][e], qr[c][e], sc[kb]);
+                    dp[kb] = mfma16(va[kb][e], dor[c][e], dp[kb]);
+                }
+        }
+        // dS in place of S: sc[kb][r] is key 16kb + 4g + r of the tile.
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float p = fast_exp2(fmaf(sc[kb][r], c2, -lse2));
+                if (DIAG && kb == NKB - 1 && 4 * g + r > i16) p = 0.0f;
+                sc[kb][r] = p * (dp[kb][r] - dl);
+            }
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const f32x4 ka = *reinterpret_cast<const f32x4 *>(&k_lds[(16 * kb + 4 * g + r) * LS + 4 * i16]);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) acc[db] = mfma16(ka[db], sc[kb][r], acc[db]);
+            }
+    };
+
+    for (;;) {
+        if (kt == 0) {
+            if (it != a.sched.wg_start[blockIdx.x]) load_rows();
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] = zero4();
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = ld_row + 16 * i;
+            *reinterpret_cast<f32x4 *>(&k_lds[row * LS + ld_col]) = kpre[i] + kb4;
+            *reinterpret_cast<f32x4 *>(&v_lds[row * LS + ld_col]) = vpre[i] + vb4;
+        }
+        __syncthreads();
+        if (pre_ok) {
+            load_tile(pbh, pkt);
+            pre_ok = advance(pit, pkt, pbh, pj);
+        }
+
+        const bool diag = kt == jq;
+        const int q0 = jq * kBwdBQ + 16 * w;
+        if (q0 < T) {  // wave-uniform
+            if (!diag) {
+                tile(IntC<4>{}, std::false_type{});
+            } else {
+                switch (w) {  // wave-uniform
+                    case 0: tile(IntC<1>{}, std::true_type{}); break;
+                    case 1: tile(IntC<2>{}, std::true_type{}); break;
+                    case 2: tile(IntC<3>{}, std::true_type{}); break;
+                    default: tile(IntC<4>{}, std::true_type{}); break;
+                }
+                if (my_q < T) {
+                    const int b = bh / a.H, h = bh - b * a.H;
+                    float *row = a.dq.p + b * a.dq.sb + my_q * a.dq.st + h * a.dq.sh + 16 * g;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        *reinterpret_cast<f32x4 *>(row + 4 * r) =
+                            f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]} * a.scale;
+                }
+            }
+        }
+        if (a.db != nullptr && diag) {
+            // db of the q part: column sums of the block's 64 dQ rows (rows
+            // < T) in a fixed order: the 16 queries of a wave (lanes of one
+            // g), then the 4 waves.  Lane (g, i16) holds dims 16g + 4r + db.
+            f32x4 cs[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool ok = q0 < T && my_q < T;
+                cs[r] = ok ? f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]} : zero4();
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) cs[r][e] += __shfl_xor(cs[r][e], off, 64);
+            }
+            if (i16 == 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) *reinterpret_cast<f32x4 *>(&red_lds[w][16 * g + 4 * r]) = cs[r] * a.scale;
+            }
+            __syncthreads();
+            if (tid < kDPad) {
+                const int b = bh / a.H, h = bh - b * a.H;
+                const float s = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
+                a.dbq_part[(static_cast<size_t>(b) * a.nqt + jq) * a.C + h * kDPad + tid] = s;
+            }
+        }
+        if (!advance(it, kt, bh, jq)) break;
+    }
+}
+
 namespace {
 
 // Key blocks are split, longest first, while the grid of key blocks and
@@ -719,7 +928,7 @@ std::pair<int, int> dkdv_slots() {
 
 int bwd_split_plan(BwdParams &p) {
     p.nsplit = 0;
-    if (!p.full || p.nqt <= kShortHeadTiles) return 0;
+    if (!p.full || p.nqt <= kShortHeadTiles || p.ds == nullptr) return 0;  // the recomputing dk/dv runs whole blocks
     const auto [per_cu, cus] = dkdv_slots();
     const auto tiles = [&](int kb) { return p.nqt - 2 * kb; };  // query tiles of key block kb
     const long long slots = static_cast<long long>(per_cu) * cus, bh = static_cast<long long>(p.B) * p.H;
@@ -780,7 +989,7 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
         hipCheck(hipEventRecord(ev[1], stream));
         hipCheck(hipEventRecord(ev[2], stream));
     }
-    if (p.full && p.nqt <= kShortHeadTiles)
+    if (p.full && (p.nqt <= kShortHeadTiles || p.ds == nullptr))
         attn_bwd_dkdv_kernel<true, true, true><<<grid_k, block, 0, stream>>>(p);
     else if (p.full)
         attn_bwd_dkdv_kernel<true, true, false><<<grid_k, block, 0, stream>>>(p);
@@ -797,7 +1006,12 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
         hipCheck(hipEventRecord(ev[3], stream));
         hipCheck(hipEventRecord(ev[4], stream));
     }
-    if (p.full) {
+    if (p.full && p.ds == nullptr) {
+        int num_wg = 0;
+        p.sched = device_block_schedule(p.B * p.H, p.nqt,
+                                        reinterpret_cast<const void *>(attn_bwd_dq16_recomp_kernel), stream, &num_wg);
+        attn_bwd_dq16_recomp_kernel<<<dim3(num_wg), block, 0, stream>>>(p);
+    } else if (p.full) {
         int num_wg = 0;
         p.sched = device_block_schedule(p.B * p.H, p.nqt, reinterpret_cast<const void *>(attn_bwd_dq16_kernel),
                                         stream, &num_wg);

@@ -299,6 +299,18 @@ void gptc_argmax_cuda(const tensor_t *logits, tensor_t *ids);
 void *gptc_stream(void);
 void gptc_set_kernel_events(void **events, int n);
 long long gptc_attention_state_floats(int B, int T, int C, int n_heads);
+
+/*
+ * gptc_attention_set_state_limit(floats): no counterpart in gpt.c.  The
+ * largest backward state (in floats) the forward keeps with the probability
+ * blocks of P'; a forward whose state would be larger keeps only the
+ * log-sum-exp (O(T) per head) when head size 64 runs, and its backward then
+ * recomputes P in both gradient kernels (7 contractions instead of 4; slower,
+ * same results to the stated tolerance).  Default and floats < 0: the int
+ * length of a tensor_t.  0 makes every D = 64 forward keep the LSE-only state.
+ * Returns the previous limit.  Applies to forwards that run after the call.
+ */
+long long gptc_attention_set_state_limit(long long floats);
 int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
                                   double *max_cu_load, int *used_pairs);
 

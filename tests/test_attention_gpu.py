@@ -270,6 +270,35 @@ def test_split_key_blocks_ragged_t(rt, oracle):
     compare_with_oracle(rt, oracle, 1, 1000, 768, 12)
 
 
+@pytest.fixture
+def lse_only_state(rt):
+    """Every D = 64 forward keeps only the log-sum-exp (state limit 0); the
+    default limit is restored afterwards."""
+    rt.lib.gptc_attention_set_state_limit(0)
+    yield
+    rt.lib.gptc_attention_set_state_limit(-1)
+
+
+@pytest.mark.parametrize("B,T,C,H", [(2, 1024, 768, 12), (1, 1000, 768, 12), (1, 200, 128, 2), (2, 100, 256, 4),
+                                     (1, 129, 128, 2), (3, 65, 128, 2), (1, 1, 64, 1)])
+def test_lse_only_state_fwd_bwd(rt, oracle, lse_only_state, B, T, C, H):
+    """The backward that recomputes P from the saved log-sum-exp in both
+    gradient kernels (dk/dv without storing dS; dq recomputing S and dP), used
+    when the probability blocks would exceed the state limit: its state is
+    O(T) per head, and its results meet the same tolerance."""
+    n = rt.lib.gptc_attention_state_floats(B, T, C, H)
+    assert n < B * H * T * 8 + B * ((T + 63) // 64) * C + 4 * B * ((T + 127) // 128) * C + 4096
+    compare_with_oracle(rt, oracle, B, T, C, H)
+
+
+def test_lse_only_state_deterministic(rt, lse_only_state):
+    x, dy = qkv_inputs(rt, 2, 300, 256, 11, 12)
+    a = run_layer(rt, x, dy, 4)
+    b = run_layer(rt, x, dy, 4)
+    for u, w in zip(a, b):
+        assert np.array_equal(u, w)
+
+
 def test_causality_at_full_length(rt):
     B, T, C, H = 2, 1024, 768, 12
     x, dy = qkv_inputs(rt, B, T, C, 21, 22)

@@ -143,6 +143,22 @@ def test_self_attention_block_matches_oracle(rt, oracle, B, T, C, H):
     On the GPU the layer folds the qkv Linear's bias into the attention
     kernels (and its gradient into their epilogues); the oracle adds it in
     the Linear, as gpt.c does."""
+    self_attention_vs_oracle(rt, oracle, B, T, C, H)
+
+
+@pytest.mark.parametrize("B,T,C,H", [(2, 256, 768, 12), (2, 100, 256, 4)])
+def test_self_attention_lse_only_state(rt, oracle, B, T, C, H):
+    """The same block with the attention state capped to the log-sum-exp: the
+    bias folded into the recomputing gradient kernels (dq's bias gradient from
+    the recomputing dq kernel's column sums)."""
+    rt.lib.gptc_attention_set_state_limit(0)
+    try:
+        self_attention_vs_oracle(rt, oracle, B, T, C, H)
+    finally:
+        rt.lib.gptc_attention_set_state_limit(-1)
+
+
+def self_attention_vs_oracle(rt, oracle, B, T, C, H):
     import oracle as oracle_mod
     ops = oracle_mod.Ops(oracle)
     rng = np.random.default_rng(5 + T)
