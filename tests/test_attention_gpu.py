@@ -291,6 +291,29 @@ def test_lse_only_state_fwd_bwd(rt, oracle, lse_only_state, B, T, C, H):
     compare_with_oracle(rt, oracle, B, T, C, H)
 
 
+def test_long_sequence_past_the_state_cap(rt, oracle):
+    """B=8 H=12 T=6700: the probability blocks would need 2.19e9 floats, past
+    the int length of a tensor_t, so the forward keeps the LSE-only state by
+    default (it refused the shape before that state existed).  Causality pins
+    the result: with dy zero past row 1024, the first 1024 rows of y and of
+    dq, dk, dv equal those of a T = 1024 run of the same rows (the
+    probability-block path), which is checked against the oracle."""
+    B, T, C, H, T0 = 8, 6700, 768, 12, 1024
+    n = rt.lib.gptc_attention_state_floats(B, T, C, H)
+    assert n < 2 * B * H * T + B * ((T + 63) // 64) * C + 4 * B * ((T + 127) // 128) * C + 4096
+    x, dy = qkv_inputs(rt, B, T, C, 41, 42)
+    dy[:, T0:] = 0.0
+    y, lse, d = run_layer(rt, x, dy, H)
+    assert np.isfinite(y).all() and np.isfinite(d).all()
+    y0, lse0, d0 = run_layer(rt, np.ascontiguousarray(x[:, :T0]), np.ascontiguousarray(dy[:, :T0]), H)
+    check("y rows < 1024 vs T=1024", y[:, :T0], y0)
+    check("lse rows < 1024", lse[:, :, :T0], lse0)
+    check("dqkv rows < 1024 vs T=1024", d[:, :T0], d0)
+    y_ref, q, k, v, att = oracle.forward(np.ascontiguousarray(x[:, :T0]), H)
+    check("y vs oracle", y0, y_ref)
+    check("dqkv vs oracle", d0, oracle.backward(np.ascontiguousarray(dy[:, :T0]), H, q, k, v, att))
+
+
 def test_lse_only_state_deterministic(rt, lse_only_state):
     x, dy = qkv_inputs(rt, 2, 300, 256, 11, 12)
     a = run_layer(rt, x, dy, 4)
