@@ -169,6 +169,16 @@ def test_reference_cache_layout(rt, oracle):
     """gpt.c's unchanged attention.c allocates q, k, v (B,H,T,D) and att (B,H,T,T)
     caches (attention.c:105-120) and passes a zeroed dout: the entry points
     must serve that layout too, leaving the same q, k, v the CPU kernel caches."""
+    reference_layout_vs_oracle(rt, oracle)
+
+
+def test_reference_cache_layout_lse_only_state(rt, oracle, lse_only_state):
+    """The same layout when the forward keeps only the log-sum-exp (D = 64
+    shapes; the D = 3 shape keeps its probability blocks)."""
+    reference_layout_vs_oracle(rt, oracle)
+
+
+def reference_layout_vs_oracle(rt, oracle):
     lib = rt.lib
     for B, T, C, H in [(2, 150, 256, 4), (2, 100, 256, 4), (2, 5, 6, 2)]:
         D = C // H
