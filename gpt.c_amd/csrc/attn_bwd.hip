@@ -15,11 +15,15 @@
 // CUs idle, bwd_split_plan), which receive exactly two atomic adds into
 // rows zeroed by the delta kernel (a + b == b + a in fp32):
 //   attn_bwd_delta_kernel  delta = rowsum(dO o O); streams dO and O once.
-//   attn_bwd_dkdv_kernel   key-parallel: per 32-key wave (V resident in
-//                          registers), over the query tiles: P from P',
-//                          dP, dS, dV += P^T dO, dK += dS^T Q.  dS
-//                          overwrites P' in place, in the exact register
-//                          layout the dq kernel consumes it in.
+//   attn_bwd_dkdv_dma_kernel  (D == 64 with the stored P') key-parallel:
+//                          per 32-key wave (V resident in registers), over
+//                          the query tiles: P from P', dP, dS,
+//                          dV += P^T dO, dK += dS^T Q.  dS overwrites P'
+//                          in place, in the exact register layout the dq
+//                          kernel consumes it in.
+//   attn_bwd_dkdv_kernel   the same for other head sizes, and with P
+//                          recomputed from the LSE (short heads, the
+//                          LSE-only state).
 //   attn_bwd_dq16_kernel   query-parallel, D == 64: dQ += dS K, 16 queries
 //                          per wave, paired 64-query blocks per workgroup.
 //   attn_bwd_dq_kernel     query-parallel, other D: dQ^T += K^T dS^T.
@@ -77,9 +81,11 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) 
     }
 }
 
-// ---- dK, dV (and the dS tiles) ----
+// ---- dK, dV (and the dS tiles): head sizes other than 64, and RECOMP ----
 // FULL: D == kDPad, 16-byte rows and 31-bit head sizes; the tile loads then
 // go through bounds-checked buffer resources (no branches, no row tests).
+// FULL is built with RECOMP only: D == 64 with the stored P' runs
+// attn_bwd_dkdv_dma_kernel.
 // RECOMP (short heads, whose forward stored no P'): P is recomputed as
 // exp2(S log2(e)/sqrt(D) - LSE log2(e)) with S = Q K^T formed like dP (Q rows
 // from LDS as A operands, this lane's K row in registers as B operands) and
@@ -94,6 +100,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RECOMP || D
                                                                      RECOMP || DP > kDPad ? 1 : 2))) void
 attn_bwd_dkdv_kernel(const BwdParams a) {
     static_assert(!FULL || DP == kDPad, "FULL kernels are built for D == 64");
+    static_assert(!FULL || RECOMP, "D == 64 with the stored P' runs attn_bwd_dkdv_dma_kernel");
     constexpr int LS = DP + 4;         // LDS row stride (floats)
     constexpr int NJ = DP / 8;         // reduction steps of 8 dims (4 per lane half)
     constexpr int NDB = DP / 32;       // 32-dim blocks of dK and dV
@@ -120,11 +127,7 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
     const int bh = blockIdx.x % a.bh_pad;
     if (bh >= a.B * a.H) return;
-    // Grid row -> key block (and part of a split one); the longest work first.
-    const int row_idx = static_cast<int>(blockIdx.x / a.bh_pad);
-    const int slot = FULL && !RECOMP && a.nsplit > 0 ? a.slot[row_idx] : 2 * row_idx;
-    const int kb_idx = slot >> 1, part = slot & 1;
-    const bool split = FULL && !RECOMP && kb_idx < a.nsplit;
+    const int kb_idx = static_cast<int>(blockIdx.x / a.bh_pad);
     const int b = bh / a.H, h = bh - b * a.H;
     const int T = a.T, D = a.D;
 
@@ -178,11 +181,9 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
         if (tid < kDPad / 4) *reinterpret_cast<f32x4 *>(&qb_lds[4 * tid]) = qb4;
     }
 
-    // Query tiles [qt0, q_end): all from the diagonal on, or one part of them.
+    // Query tiles [qt0, n_qt): all from the diagonal on.
     const int n_qt = a.nqt;
-    const int qt_diag = k_blk0 / kBwdBQ, q_mid = qt_diag + (n_qt - qt_diag + 1) / 2;
-    const int qt0 = split && part ? q_mid : qt_diag;
-    const int q_end = split && !part ? q_mid : n_qt;
+    const int qt0 = k_blk0 / kBwdBQ, q_end = n_qt;
     const int ld_row = tid / TPR, ld_col = 4 * (tid % TPR);
     const auto q_rows = head_rows(Qh, T, a.q.st);
     const auto do_rows = head_rows(dOh, T, a.dout.st);
@@ -369,13 +370,8 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
         for (int r = 0; r < 16; ++r) {
             const int key = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3);
             if (key < T) {
-                if (split) {
-                    unsafeAtomicAdd(&dKh[key * a.dk.st + dim], acc_dk[db][r] * a.scale);
-                    unsafeAtomicAdd(&dVh[key * a.dv.st + dim], acc_dv[db][r]);
-                } else {
-                    dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
-                    dVh[key * a.dv.st + dim] = acc_dv[db][r];
-                }
+                dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
+                dVh[key * a.dv.st + dim] = acc_dv[db][r];
             }
         }
     }
@@ -403,6 +399,261 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
             const float s = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
             // Row (b, key block or its part 1) of the (B*(nkb + nsplit)) x 2C
             // partials: dk part, then dv part.
+            const int col = (tid < kDPad ? 0 : a.C) + h * kDPad + (tid & (kDPad - 1));
+            a.dbkv_part[(static_cast<size_t>(b) * a.nkb + kb_idx) * 2 * a.C + col] = s;
+        }
+    }
+}
+
+// ---- dK, dV of D == 64 heads with the stored P' (the long-head path) ----
+// The same per-wave work as attn_bwd_dkdv_kernel<true, true, false>, with the
+// Q and dO tiles double-buffered in LDS and filled by buffer loads that write
+// LDS directly (one row of 64 floats per instruction, lanes -> consecutive
+// dims; rows past T read as zeros through the buffer resource).  Tile qt + 1
+// is requested right after the barrier that opens tile qt, so one barrier per
+// tile both publishes the next tile and frees the previous one, and the tile
+// loads take no registers and no LDS store instructions.
+//
+// The compiler does not see these loads: the wait for them is an explicit
+// s_waitcnt vmcnt(0) (through the builtin, so that the compiler's own
+// counting knows every earlier load has landed) right before that barrier.
+// Loads the compiler issues later are younger than the tile's, so its own
+// waits can only over-wait, never under-wait.
+//
+// BIAS: the q bias is added to the Q operand of dK += dS^T Q as it is read
+// (the same sum as adding it to the stored tile: rows past T then hold the
+// bias, with dS = 0 there).
+template <bool BIAS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_bwd_dkdv_dma_kernel(const BwdParams a) {
+    constexpr int LS = kDPad + 4;      // LDS row stride (floats)
+    constexpr int NJ = kDPad / 8;      // reduction steps of 8 dims (4 per lane half)
+    constexpr int kTile = kBwdBQ * LS;  // floats per LDS tile
+    __shared__ __attribute__((aligned(16))) float q_lds[2 * kTile];
+    __shared__ __attribute__((aligned(16))) float do_lds[2 * kTile];
+    // Per buffer, one entry per thread: [0, 128) the factors f of P = P' * f
+    // for the workgroup's two 64-key tiles ([key tile][query]), [128, 192)
+    // delta, [192, 256) unused.
+    __shared__ __attribute__((aligned(16))) float stat_lds[2 * 256];
+    __shared__ float red_lds[4][2 * kDPad];
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
+    const int bh = blockIdx.x % a.bh_pad;
+    if (bh >= a.B * a.H) return;
+    const int row_idx = static_cast<int>(blockIdx.x / a.bh_pad);
+    const int slot = a.nsplit > 0 ? a.slot[row_idx] : 2 * row_idx;
+    const int kb_idx = slot >> 1, part = slot & 1;
+    const bool split = kb_idx < a.nsplit;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int T = a.T;
+
+    const int k_blk0 = kb_idx * kBwdBK;
+    const int kw0 = k_blk0 + 32 * w;
+    const int my_k = kw0 + l32;
+    const bool k_ok = my_k < T;
+
+    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
+    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
+    const float *dOh = a.dout.p + b * a.dout.sb + h * a.dout.sh;
+    const float *lse_h = a.lse + static_cast<uint32_t>(bh) * T;
+    const float *dl_h = a.delta + static_cast<uint32_t>(bh) * T;
+    const float *pm_h = a.pm + static_cast<uint32_t>(bh) * a.nqt * T;
+
+    // V row of this lane's key, dims 8j + 4hf + c: B operand of dP = dO V^T.
+    f32x4 vr[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) vr[j] = k_ok ? load4<true>(Vh + my_k * a.v.st, 8 * j + 4 * hf, kDPad) : zero4();
+    // BIAS: the v bias joins this key's V row (keys past T keep a zero row);
+    // the q bias of this lane's two dims joins the Q operand below.
+    f32x4 vbias[NJ];
+    float qbias[2] = {0.0f, 0.0f};
+    if (BIAS) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) vbias[j] = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 8 * j + 4 * hf);
+        qbias[0] = a.qb[h * kDPad + l32];
+        qbias[1] = a.qb[h * kDPad + 32 + l32];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (BIAS && k_ok) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) vr[j] += vbias[j];
+    }
+
+    const int n_qt = a.nqt;
+    const int qt_diag = k_blk0 / kBwdBQ, q_mid = qt_diag + (n_qt - qt_diag + 1) / 2;
+    const int qt0 = split && part ? q_mid : qt_diag;
+    const int q_end = split && !part ? q_mid : n_qt;
+    const auto q_rows = head_rows(Qh, T, a.q.st);
+    const auto do_rows = head_rows(dOh, T, a.dout.st);
+
+    // Rows 16w .. 16w+15 of tile qt into LDS buffer buf (M0 = the row's LDS byte address).
+    const uint32_t vl = 4u * lane;
+    const uint32_t lds_q = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                               (__attribute__((address_space(3))) float *)q_lds)) + 16u * w * LS * 4u);
+    const uint32_t lds_do = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                                (__attribute__((address_space(3))) float *)do_lds)) + 16u * w * LS * 4u);
+    auto load_tile = [&](int qt, int buf) {
+        const uint32_t q0 = static_cast<uint32_t>(qt * kBwdBQ + 16 * w);
+        const uint32_t mq = lds_q + buf * (kTile * 4u), md = lds_do + buf * (kTile * 4u);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t q = q0 + i;
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(mq + i * LS * 4u),
+                         "v"(q * a.q.st * 4u + vl), "s"(q_rows)
+                         : "memory");
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(md + i * LS * 4u),
+                         "v"(q * a.dout.st * 4u + vl), "s"(do_rows)
+                         : "memory");
+        }
+    };
+    // The statistics of a tile, loaded one tile ahead (see attn_bwd_dkdv_kernel).
+    float st0 = 0.0f, st1 = 0.0f;
+    bool st_ok = false;
+    auto load_stats = [&](int qt) {
+        const int q = qt * kBwdBQ + (tid & (kBwdBQ - 1));
+        const int qc = min(q, T - 1);
+        const bool is_m = tid < 2 * kBwdBQ;
+        const int kt = 2 * kb_idx + ((tid >> 6) & 1);
+        st_ok = q < T && (!is_m || kt < n_qt);
+        st0 = *(is_m ? pm_h + min(kt, n_qt - 1) * T + qc : dl_h + qc);
+        st1 = lse_h[qc];
+    };
+
+    float pbuf[16];
+    auto half_needed = [&](int qt, int qb) {
+        const int qh0 = qt * kBwdBQ + 32 * qb;
+        return qh0 + 31 >= kw0 && kw0 < T && qh0 < T;
+    };
+    const uint32_t lane_off = 4 * hf * 32 + l32;
+    auto half_base = [&](int qt, int qb) {
+        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh, n_qt, qt, kw0 >> 5)) + 32 * qb * 32);
+    };
+    auto load_p = [&](int qt, int qb) {
+        if (!half_needed(qt, qb)) return;
+        const float *hb = half_base(qt, qb);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
+    };
+    if (qt0 < q_end) {
+        load_tile(qt0, 0);
+        load_stats(qt0);
+        load_p(qt0, 0);
+    }
+
+    f32x16 acc_dk[2], acc_dv[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db) acc_dk[db] = acc_dv[db] = zero16();
+
+    for (int qt = qt0, buf = 0; qt < q_end; ++qt, buf ^= 1) {
+        {
+            const float f = fast_exp2(st0 - st1 * kLog2e);
+            stat_lds[buf * 256 + tid] = st_ok ? (tid < 2 * kBwdBQ ? f : st0) : 0.0f;
+        }
+        // This wave's loads of tile qt have landed; after the barrier every
+        // wave's have, and tile qt - 1 (the other buffer) is no longer read.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (qt + 1 < q_end) load_tile(qt + 1, buf ^ 1);
+
+        const float *qs = q_lds + buf * kTile, *dos = do_lds + buf * kTile;
+        const float *f_w = stat_lds + buf * 256 + (w >> 1) * kBwdBQ;
+        const float *dl_w = stat_lds + buf * 256 + 2 * kBwdBQ;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const bool need = half_needed(qt, qb);
+            f32x16 s, dp = zero16();
+            if (need) {
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const f32x4 da = *reinterpret_cast<const f32x4 *>(&dos[(32 * qb + l32) * LS + 8 * j + 4 * hf]);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) dp = mfma32(da[c], vr[j][c], dp);
+                }
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 f4 = *reinterpret_cast<const f32x4 *>(&f_w[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) s[4 * g + c] = pbuf[4 * g + c] * f4[c];  // P
+                }
+            }
+            if (qb == 0) {
+                load_p(qt, 1);
+                if (qt + 1 < q_end) load_stats(qt + 1);
+            } else if (qt + 1 < q_end) {
+                load_p(qt + 1, 0);
+            }
+            if (!need) continue;
+
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&dl_w[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) dp[4 * g + c] = s[4 * g + c] * (dp[4 * g + c] - d4[c]);  // dS
+            }
+            {
+                float *hb = half_base(qt, qb);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int row = 32 * qb + 8 * g + 4 * hf + c;
+#pragma unroll
+                    for (int db = 0; db < 2; ++db) {
+                        const float qv = qs[row * LS + 32 * db + l32];
+                        acc_dv[db] = mfma32(s[4 * g + c], dos[row * LS + 32 * db + l32], acc_dv[db]);
+                        acc_dk[db] = mfma32(dp[4 * g + c], BIAS ? qv + qbias[db] : qv, acc_dk[db]);
+                    }
+                }
+        }
+    }
+
+    // Accumulator layout (keys x dims): lane -> dim 32*db + l32,
+    // register r -> key kw0 + 8(r/4) + 4hf + r%4.
+    float *dKh = a.dk.p + b * a.dk.sb + h * a.dk.sh;
+    float *dVh = a.dv.p + b * a.dv.sb + h * a.dv.sh;
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+        const int dim = 32 * db + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            if (key < T) {
+                if (split) {
+                    unsafeAtomicAdd(&dKh[key * a.dk.st + dim], acc_dk[db][r] * a.scale);
+                    unsafeAtomicAdd(&dVh[key * a.dv.st + dim], acc_dv[db][r]);
+                } else {
+                    dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
+                    dVh[key * a.dv.st + dim] = acc_dv[db][r];
+                }
+            }
+        }
+    }
+    if (a.db != nullptr) {
+        // db of the k and v parts, as in attn_bwd_dkdv_kernel.
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+            float sk = 0.0f, sv = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const bool ok = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3) < T;
+                sk += ok ? acc_dk[db][r] : 0.0f;
+                sv += ok ? acc_dv[db][r] : 0.0f;
+            }
+            sk += other_half(sk);
+            sv += other_half(sv);
+            if (hf == 0) {
+                red_lds[w][32 * db + l32] = sk * a.scale;
+                red_lds[w][kDPad + 32 * db + l32] = sv;
+            }
+        }
+        __syncthreads();
+        if (tid < 2 * kDPad) {
+            const float s = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
             const int col = (tid < kDPad ? 0 : a.C) + h * kDPad + (tid & (kDPad - 1));
             const int prow = split && part ? a.nkb + kb_idx : kb_idx;
             a.dbkv_part[(static_cast<size_t>(b) * (a.nkb + a.nsplit) + prow) * 2 * a.C + col] = s;
@@ -917,7 +1168,7 @@ std::pair<int, int> dkdv_slots() {
     if (it == g_dkdv_slots.end()) {
         int per_cu = 0, cus = 0;
         hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void *>(attn_bwd_dkdv_kernel<true, true, false>), 256, 0));
+            &per_cu, reinterpret_cast<const void *>(attn_bwd_dkdv_dma_kernel<false>), 256, 0));
         hipCheck(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         it = g_dkdv_slots.emplace(dev, std::make_pair(std::max(1, per_cu), std::max(1, cus))).first;
     }
@@ -991,8 +1242,10 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
     }
     if (p.full && (p.nqt <= kShortHeadTiles || p.ds == nullptr))
         attn_bwd_dkdv_kernel<true, true, true><<<grid_k, block, 0, stream>>>(p);
+    else if (p.full && p.qb != nullptr)
+        attn_bwd_dkdv_dma_kernel<true><<<grid_k, block, 0, stream>>>(p);
     else if (p.full)
-        attn_bwd_dkdv_kernel<true, true, false><<<grid_k, block, 0, stream>>>(p);
+        attn_bwd_dkdv_dma_kernel<false><<<grid_k, block, 0, stream>>>(p);
     else if (wide && p.vec)
         attn_bwd_dkdv_kernel<true, false, false, 2 * kDPad><<<grid_k, block, 0, stream>>>(p);
     else if (wide)

@@ -127,6 +127,10 @@ __device__ __forceinline__ void store4(float *row, int dim, int D, f32x4 v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// s_waitcnt immediate that waits for vmcnt == 0 only (gfx9 encoding:
+// vmcnt [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]; the others at their maxima).
+constexpr int kWaitVmcnt0 = 0x0F70;
+
 // Value held by the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32, 64); }
 
