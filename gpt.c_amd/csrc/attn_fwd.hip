@@ -674,27 +674,28 @@ attn_fwd_short_kernel(const FwdParams a) {
 // ---- Two-tile heads (64 < T <= 128, D == 64, compact layout) ----
 //
 // A head of two 64-query blocks is 36 units of MFMA work, a unit being one
-// 16-query slab against one 16-key block: the second block's four slabs
-// see 4 + 1, 4 + 2, 4 + 3 and 4 + 4 units (its full first tile, then its
-// diagonal tile), the first block's 1, 2, 3 and 4.  With one workgroup per
-// block (the kernel above) the last wave of the second block carries 8 in a
-// row, one wave per SIMD.  Here two workgroups per head share the 36 units
-// so that no wave carries more than 5; a slab whose two tiles run on two
-// waves has its partial softmax state (running max, sums, O) merged through
-// LDS after the workgroup's one barrier of the compute phase:
-//   role 0: w0 slab (1,3) tile 0 -> partial 0; w1 slab (1,3) diagonal, merges 0;
-//           w2 slab (1,0) both tiles; w3 slabs (0,3) and (0,0)
-//   role 1: w0 slab (1,1) tile 0 -> partial 0; w1 slab (1,2) tile 0 -> partial 1;
-//           w2 slab (0,1), then (1,2) diagonal, merges 1;
-//           w3 slab (0,2), then (1,1) diagonal, merges 0
-// (slab (j, s): queries 64j + 16s .. 64j + 16s + 15).  Both workgroups stage
-// the head's two K/V tiles.
+// 16-query slab against one 16-key block: slab (j, s) (queries 64j + 16s ..
+// 64j + 16s + 15) sees key blocks 0 .. 4j + s, the last of them its
+// diagonal, so the second block's slabs carry 5 .. 8 units and the first
+// block's 1 .. 4.  Four workgroups per head, each one long and one short
+// slab (9 units), and every slab cut into pieces of at most 3 consecutive
+// key blocks, one piece per wave: no wave carries more than 3 units (96
+// MFMAs).  The pieces of a slab merge their partial softmax states (running
+// max, sums, O) through LDS after the workgroup's one barrier of the compute
+// phase, in a fixed order.
+//   role 0: slabs (1,3) [blocks 0-2 | 3-5 | 6-7] and (0,0) [0]
+//   role 1: slabs (1,2) [0-2 | 3-5 | 6] and (0,1) [0-1]
+//   role 2: slabs (1,1) [0-2 | 3-5] and (0,2) [0-2]
+//   role 3: slabs (1,0) [0-2 | 3-4] and (0,3) [0-1 | 2-3]
+// Every workgroup stages the head's two K/V tiles (key k in LDS row k).
 struct SlabState {
     float m_run, l_run;
     f32x4 acc[4];
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+constexpr int kTwoTileRoles = 4;  // workgroups per head
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 attn_fwd_twotile_kernel(const FwdParams a) {
     constexpr int TILE = kFwdBN * kLdsStride;
     __shared__ __attribute__((aligned(16))) float k_lds[2 * TILE];
@@ -705,26 +706,17 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
     const int BH = a.B * a.H, T = a.T;
-    const int role = static_cast<int>(blockIdx.x) / BH;  // grid = 2 * BH
+    const int role = static_cast<int>(blockIdx.x) / BH;  // grid = kTwoTileRoles * BH
     const int bh = static_cast<int>(blockIdx.x) - role * BH;
     const int b = bh / a.H, h = bh - b * a.H;
 
     const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
     const auto k_rows = head_rows(a.k.p + b * a.k.sb + h * a.k.sh, T, a.k.st);
     const auto v_rows = head_rows(a.v.p + b * a.v.sb + h * a.v.sh, T, a.v.st);
-    // This wave's slabs (first, second): (block j, slab s) as listed above.
+    // This wave's slab (block j, slab s); the wave of role 2 with no piece has none.
     const int job = 4 * role + w;  // wave-uniform
-    constexpr int kJobSlabs[8][4] = {{1, 3, -1, 0}, {1, 3, -1, 0}, {1, 0, -1, 0}, {0, 3, 0, 0},
-                                     {1, 1, -1, 0}, {1, 2, -1, 0}, {0, 1, 1, 2}, {0, 2, 1, 1}};
-    // The Q rows of the wave's slabs (loaded after the K/V staging: issuing
-    // them first measured no faster, warm or cold).
-    f32x4 qa[4], qb[4];
-    auto load_q = [&](int j, int sl, f32x4(&qr)[4]) {
-        const int q = j * kF16Rows + 16 * sl + i16;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c);
-    };
-    const bool two_slabs = kJobSlabs[job][2] >= 0;
+    constexpr int kJobSlab[16][2] = {{1, 3}, {1, 3}, {1, 3}, {0, 0}, {1, 2}, {1, 2}, {1, 2}, {0, 1},
+                                     {1, 1}, {1, 1}, {0, 2}, {-1, 0}, {1, 0}, {1, 0}, {0, 3}, {0, 3}};
     const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
     f32x4 kpre[2][4], vpre[2][4];
 #pragma unroll
@@ -755,34 +747,35 @@ attn_fwd_twotile_kernel(const FwdParams a) {
             *reinterpret_cast<f32x4 *>(&k_lds[kt * TILE + row * kLdsStride + ld_col]) = kpre[kt][i] + kb4;
             *reinterpret_cast<f32x4 *>(&v_lds[kt * TILE + row * kLdsStride + ld_col]) = vpre[kt][i] + vb4;
         }
+    // The Q rows of the wave's slab, with the q bias (issued after the K/V
+    // loads: issuing them first measured no faster, warm or cold).
+    const int sj = kJobSlab[job][0], ss = kJobSlab[job][1];
+    f32x4 qr[4];
+    if (sj >= 0) {
+        const int q = sj * kF16Rows + 16 * ss + i16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c) + qb4[c];
+    }
     __syncthreads();
 
     const float c2 = a.scale_log2;
-    f32x4 qr[4];
-    // Q of the wave's first (second) slab, with the q bias.
-    auto use_q = [&](const f32x4(&src)[4]) {
+    SlabState st;
+    st.m_run = -INFINITY;
+    st.l_run = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qr[c] = src[c] + qb4[c];
-    };
-    auto fresh = [](SlabState &st) {
-        st.m_run = -INFINITY;
-        st.l_run = 0.0f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) st.acc[db] = zero4();
-    };
+    for (int db = 0; db < 4; ++db) st.acc[db] = zero4();
     f32x4 sc[4];
-    auto full_tile0 = [&](SlabState &st) {
-        fwd16_scores<4, false>(k_lds, qr, g, i16, c2, st.m_run, st.l_run, st.acc, sc);
-        fwd16_pv<4>(v_lds, sc, g, i16, st.acc);
+    // Key blocks KB0 .. KB0 + NKB - 1 of the wave's slab (DIAG: the last is the
+    // slab's diagonal block, masked per key).
+    auto piece = [&](auto kb0_c, auto nkb_c, auto diag_c) {
+        constexpr int KB0 = decltype(kb0_c)::value, NKB = decltype(nkb_c)::value;
+        constexpr bool DIAG = decltype(diag_c)::value;
+        fwd16_scores<NKB, DIAG>(k_lds + 16 * KB0 * kLdsStride, qr, g, i16, c2, st.m_run, st.l_run, st.acc, sc);
+        fwd16_pv<NKB>(v_lds + 16 * KB0 * kLdsStride, sc, g, i16, st.acc);
     };
-    // Slab s of block j against its diagonal tile j: key blocks 0 .. s, the last masked per key.
-    auto diag = [&](auto s_c, int j, SlabState &st) {
-        constexpr int NKB = decltype(s_c)::value + 1;
-        fwd16_scores<NKB, true>(k_lds + j * TILE, qr, g, i16, c2, st.m_run, st.l_run, st.acc, sc);
-        fwd16_pv<NKB>(v_lds + j * TILE, sc, g, i16, st.acc);
-    };
-    auto finish = [&](int j, int sl, const SlabState &st) {
-        const int my_q = j * kF16Rows + 16 * sl + i16;
+    auto finish = [&]() {
+        const int my_q = sj * kF16Rows + 16 * ss + i16;
         const float lt = sum4_rows(st.l_run);
         if (my_q < T) {
             const float inv = 1.0f / lt;
@@ -797,14 +790,14 @@ attn_fwd_twotile_kernel(const FwdParams a) {
             if (g == 0) a.lse[static_cast<uint32_t>(bh) * T + my_q] = (st.m_run + log2f(lt)) * kLn2;
         }
     };
-    auto put_partial = [&](int slot, const SlabState &st) {
+    auto put_partial = [&](int slot) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) part_lds[slot][db][lane] = st.acc[db];
         part_lds[slot][4][lane] = f32x4{st.m_run, st.l_run, 0.0f, 0.0f};
     };
-    // st (the diagonal tile) merged with partial `slot` (the full tile 0):
-    // both running maxima are finite (every query sees key 0 and its own key).
-    auto merge = [&](int slot, SlabState &st) {
+    // The state merged with partial `slot`: both running maxima are finite
+    // (every piece holds at least one key each of its queries sees).
+    auto merge = [&](int slot) {
         const f32x4 ml = part_lds[slot][4][lane];
         const float m = fmaxf(st.m_run, ml[0]);
         const float fa = fast_exp2(st.m_run - m), fb = fast_exp2(ml[0] - m);
@@ -814,37 +807,35 @@ attn_fwd_twotile_kernel(const FwdParams a) {
         st.m_run = m;
     };
 
-    load_q(kJobSlabs[job][0], kJobSlabs[job][1], qa);
-    if (two_slabs) load_q(kJobSlabs[job][2], kJobSlabs[job][3], qb);
-    SlabState st;
-    fresh(st);
-    use_q(qa);
-    // Compute phase: at most 5 units per wave.
+    // Compute phase: at most 3 units per wave.
+    using F = std::false_type;
+    using D = std::true_type;
     switch (job) {
-        case 0: full_tile0(st); put_partial(0, st); break;
-        case 1: diag(IntC<3>{}, 1, st); break;
-        case 2: full_tile0(st); diag(IntC<0>{}, 1, st); finish(1, 0, st); break;
-        case 3:
-            diag(IntC<3>{}, 0, st); finish(0, 3, st);
-            fresh(st); use_q(qb); diag(IntC<0>{}, 0, st); finish(0, 0, st);
-            break;
-        case 4: full_tile0(st); put_partial(0, st); break;
-        case 5: full_tile0(st); put_partial(1, st); break;
-        case 6:
-            diag(IntC<1>{}, 0, st); finish(0, 1, st);
-            fresh(st); use_q(qb); diag(IntC<2>{}, 1, st);
-            break;
-        default:
-            diag(IntC<2>{}, 0, st); finish(0, 2, st);
-            fresh(st); use_q(qb); diag(IntC<1>{}, 1, st);
-            break;
+        case 0: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
+        case 1: piece(IntC<3>{}, IntC<3>{}, F{}); put_partial(1); break;
+        case 2: piece(IntC<6>{}, IntC<2>{}, D{}); break;
+        case 3: piece(IntC<0>{}, IntC<1>{}, D{}); finish(); break;
+        case 4: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
+        case 5: piece(IntC<3>{}, IntC<3>{}, F{}); put_partial(1); break;
+        case 6: piece(IntC<6>{}, IntC<1>{}, D{}); break;
+        case 7: piece(IntC<0>{}, IntC<2>{}, D{}); finish(); break;
+        case 8: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
+        case 9: piece(IntC<3>{}, IntC<3>{}, D{}); break;
+        case 10: piece(IntC<0>{}, IntC<3>{}, D{}); finish(); break;
+        case 11: break;
+        case 12: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
+        case 13: piece(IntC<3>{}, IntC<2>{}, D{}); break;
+        case 14: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(1); break;
+        default: piece(IntC<2>{}, IntC<2>{}, D{}); break;
     }
     __syncthreads();
-    // Merge phase.
+    // Merge phase: the diagonal piece of a split slab takes in the others.
     switch (job) {
-        case 1: merge(0, st); finish(1, 3, st); break;
-        case 6: merge(1, st); finish(1, 2, st); break;
-        case 7: merge(0, st); finish(1, 1, st); break;
+        case 2:
+        case 6: merge(0); merge(1); finish(); break;
+        case 9:
+        case 13: merge(0); finish(); break;
+        case 15: merge(1); finish(); break;
         default: break;
     }
 }
@@ -861,7 +852,7 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
         if (deep && !perm) {
             if (ev) hipCheck(hipEventRecord(ev[0], stream));
             if (p.nqt == 2)
-                attn_fwd_twotile_kernel<<<dim3(2 * p.B * p.H), dim3(256), 0, stream>>>(p);
+                attn_fwd_twotile_kernel<<<dim3(kTwoTileRoles * p.B * p.H), dim3(256), 0, stream>>>(p);
             else
                 attn_fwd_short_kernel<<<dim3(p.B * p.H * p.nqt), dim3(256), 0, stream>>>(p);
             hipCheck(hipGetLastError());
