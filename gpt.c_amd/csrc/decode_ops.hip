@@ -43,13 +43,56 @@ struct RowsArgs {
 // computed by the workgroup: the decode step's rows are at most 8 of a few
 // thousand features).  kPer > 1 (wide outputs): a wave reads its normalised
 // x vector once for kPer weight rows, with kPer loads in flight.
+//
+// A step is a chain of short kernels, so each one's time is mostly memory
+// latency: everything that does not depend on the LayerNorm statistics (the
+// wave's first kIt 16-byte weight vectors, the LayerNorm weights, the bias
+// and residual of the output this thread finishes) is requested before
+// them, and the sums keep the order of a plain loop over the inputs.
 template <bool kVec, bool kLN, int kOuts, int kPer>
 __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a) {
     constexpr int kSplit = kWaves / kOuts;
+    constexpr int kIt = 4;  // 16-byte steps per lane loaded up front (in_f <= 1024 kSplit)
     __shared__ float part[kWaves * kPer][kMaxRows];
     __shared__ float stat[2][kMaxRows];
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     const int in_f = a.in_f, rows = a.rows;
+    const int grp = w / kSplit, slice = w % kSplit;
+    const int o0 = (blockIdx.x * kOuts + grp) * kPer;  // this wave's first output
+    const int per = (in_f + kSplit - 1) / kSplit;
+    const int j0 = slice * per, j1 = min(in_f, j0 + per);
+
+    // The bias and residual of the (output, row) this thread finishes.
+    const int n_fin = kOuts * kPer * rows;
+    float fin_b = 0.0f, fin_r = 0.0f;
+    if (static_cast<int>(threadIdx.x) < n_fin) {
+        const int oo = threadIdx.x / rows, r = threadIdx.x % rows;
+        const int out = blockIdx.x * kOuts * kPer + oo;
+        if (out < a.out_f) {
+            if (a.b != nullptr) fin_b = a.b[out];
+            if (a.res != nullptr) fin_r = a.res[static_cast<int64_t>(r) * a.out_f + out];
+        }
+    }
+    // kVec: the wave's first kIt weight vectors per output (and LayerNorm vectors).
+    const int jb = j0 / 4 + lane, je = j1 / 4;
+    f32x4_t wv[kIt][kPer], lw[kIt], lb[kIt];
+    if (kVec && o0 < a.out_f) {
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int j = jb + it * kWave;
+#pragma unroll
+            for (int p = 0; p < kPer; ++p)
+                wv[it][p] = j < je && o0 + p < a.out_f
+                                ? reinterpret_cast<const f32x4_t *>(a.W + static_cast<int64_t>(o0 + p) * in_f)[j]
+                                : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            lw[it] = f32x4_t{1.0f, 1.0f, 1.0f, 1.0f};
+            lb[it] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if (kLN && j < je) {
+                lw[it] = reinterpret_cast<const f32x4_t *>(a.ln_w)[j];
+                if (a.ln_b != nullptr) lb[it] = reinterpret_cast<const f32x4_t *>(a.ln_b)[j];
+            }
+        }
+    }
     if (kLN) {
         // Mean and E[x^2] - mean^2 of each row, as layer_norm_forward_cuda_kernel
         // (and gpt.c's LayerNorm.c) compute them; wave r handles rows r, r+4, ...
@@ -58,11 +101,11 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
             float s = 0.0f, ss = 0.0f;
             if (kVec) {  // 16-byte loads, all of a lane's loads issued together
                 constexpr int kU = 4;
-                for (int j0 = lane; j0 < in_f / 4; j0 += kU * kWave) {
+                for (int j0s = lane; j0s < in_f / 4; j0s += kU * kWave) {
                     f32x4_t v[kU];
 #pragma unroll
                     for (int u = 0; u < kU; ++u) {
-                        const int j = j0 + u * kWave;
+                        const int j = j0s + u * kWave;
                         v[u] = j < in_f / 4 ? reinterpret_cast<const f32x4_t *>(xr)[j] : f32x4_t{0, 0, 0, 0};
                     }
 #pragma unroll
@@ -91,10 +134,6 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
         }
         __syncthreads();
     }
-    const int grp = w / kSplit, slice = w % kSplit;
-    const int o0 = (blockIdx.x * kOuts + grp) * kPer;  // this wave's first output
-    const int per = (in_f + kSplit - 1) / kSplit;
-    const int j0 = slice * per, j1 = min(in_f, j0 + per);
     float acc[kPer][kMaxRows];
 #pragma unroll
     for (int p = 0; p < kPer; ++p)
@@ -102,35 +141,42 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
         for (int r = 0; r < kMaxRows; ++r) acc[p][r] = 0.0f;
     if (o0 < a.out_f) {
         if (kVec) {  // in_f % (4 kSplit) == 0: slices are whole 16-byte vectors
-            for (int j = j0 / 4 + lane; j < j1 / 4; j += kWave) {
-                f32x4_t wv[kPer];
-#pragma unroll
-                for (int p = 0; p < kPer; ++p)
-                    wv[p] = o0 + p < a.out_f
-                                ? reinterpret_cast<const f32x4_t *>(a.W + static_cast<int64_t>(o0 + p) * in_f)[j]
-                                : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                f32x4_t lw = {1.0f, 1.0f, 1.0f, 1.0f}, lb = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (kLN) {
-                    lw = reinterpret_cast<const f32x4_t *>(a.ln_w)[j];
-                    if (a.ln_b != nullptr) lb = reinterpret_cast<const f32x4_t *>(a.ln_b)[j];
-                }
+            auto step = [&](int j, const f32x4_t(&w4)[kPer], const f32x4_t &lw4, const f32x4_t &lb4) {
 #pragma unroll
                 for (int r = 0; r < kMaxRows; ++r) {
                     if (r < rows) {
                         f32x4_t xv = reinterpret_cast<const f32x4_t *>(a.x + static_cast<int64_t>(r) * in_f)[j];
                         if (kLN) {
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) xv[e] = (xv[e] - stat[0][r]) * stat[1][r] * lw[e] + lb[e];
+                            for (int e = 0; e < 4; ++e) xv[e] = (xv[e] - stat[0][r]) * stat[1][r] * lw4[e] + lb4[e];
                         }
 #pragma unroll
                         for (int p = 0; p < kPer; ++p) {
-                            acc[p][r] = fmaf(wv[p][0], xv[0], acc[p][r]);
-                            acc[p][r] = fmaf(wv[p][1], xv[1], acc[p][r]);
-                            acc[p][r] = fmaf(wv[p][2], xv[2], acc[p][r]);
-                            acc[p][r] = fmaf(wv[p][3], xv[3], acc[p][r]);
+                            acc[p][r] = fmaf(w4[p][0], xv[0], acc[p][r]);
+                            acc[p][r] = fmaf(w4[p][1], xv[1], acc[p][r]);
+                            acc[p][r] = fmaf(w4[p][2], xv[2], acc[p][r]);
+                            acc[p][r] = fmaf(w4[p][3], xv[3], acc[p][r]);
                         }
                     }
                 }
+            };
+#pragma unroll
+            for (int it = 0; it < kIt; ++it)
+                if (jb + it * kWave < je) step(jb + it * kWave, wv[it], lw[it], lb[it]);
+            // Inputs past the first kIt steps (in_f > 1024 kSplit): streamed.
+            for (int j = jb + kIt * kWave; j < je; j += kWave) {
+                f32x4_t w4[kPer];
+#pragma unroll
+                for (int p = 0; p < kPer; ++p)
+                    w4[p] = o0 + p < a.out_f
+                                ? reinterpret_cast<const f32x4_t *>(a.W + static_cast<int64_t>(o0 + p) * in_f)[j]
+                                : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                f32x4_t lw4 = {1.0f, 1.0f, 1.0f, 1.0f}, lb4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (kLN) {
+                    lw4 = reinterpret_cast<const f32x4_t *>(a.ln_w)[j];
+                    if (a.ln_b != nullptr) lb4 = reinterpret_cast<const f32x4_t *>(a.ln_b)[j];
+                }
+                step(j, w4, lw4, lb4);
             }
         } else {
             for (int j = j0 + lane; j < j1; j += kWave) {
@@ -159,16 +205,17 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
             }
     __syncthreads();
     // One thread per (output, row) adds the slices in order and finishes.
-    for (int t = threadIdx.x; t < kOuts * kPer * rows; t += kThreads) {
+    for (int t = threadIdx.x; t < n_fin; t += kThreads) {
         const int oo = t / rows, r = t % rows;
         const int out = blockIdx.x * kOuts * kPer + oo;
         if (out < a.out_f) {
             float v = part[oo * kSplit][r];
 #pragma unroll
             for (int s = 1; s < kSplit; ++s) v += part[oo * kSplit + s][r];
-            if (a.b != nullptr) v += a.b[out];
+            const bool first = t == static_cast<int>(threadIdx.x);
+            if (a.b != nullptr) v += first ? fin_b : a.b[out];
             if (a.act == 1) v = gelu_tanh(v);
-            if (a.res != nullptr) v += a.res[static_cast<int64_t>(r) * a.out_f + out];
+            if (a.res != nullptr) v += first ? fin_r : a.res[static_cast<int64_t>(r) * a.out_f + out];
             a.y[static_cast<int64_t>(r) * a.out_f + out] = v;
         }
     }
