@@ -272,10 +272,11 @@ __global__ __launch_bounds__(kThreads) void embed_token_kernel(const float *__re
 
 constexpr int kArgThreads = 1024;
 constexpr int kArgWaves = kArgThreads / kWave;
+constexpr int kArgU = 16;  // elements per thread per round, loads issued together
 
 // ids[r] = the first index of the largest value of logits row r (NaN never wins).
-// 1024 threads; each takes 4 strided elements per round with the 4 loads
-// issued together, so a 50257-wide row is about 13 memory round trips.
+// 1024 threads; each takes kArgU strided elements per round with all their
+// loads issued together, so a 50257-wide row is 4 memory round trips.
 // With pos_dev set, the token goes to ids[r * stride + *pos_dev + 1], and only
 // once the prompt (positions < prompt) has been consumed and while it is
 // below total.
@@ -287,15 +288,15 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__rest
     const float *row = logits + static_cast<int64_t>(blockIdx.x) * V;
     float best = -INFINITY;
     int bi = V;  // none yet
-    for (int j0 = threadIdx.x; j0 < V; j0 += 4 * kArgThreads) {
-        float v[4];
+    for (int j0 = threadIdx.x; j0 < V; j0 += kArgU * kArgThreads) {
+        float v[kArgU];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kArgU; ++u) {
             const int j = j0 + u * kArgThreads;
             v[u] = j < V ? row[j] : -INFINITY;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < kArgU; ++u)
             if (v[u] > best) {  // strictly greater, indices rising: keeps the first index per thread
                 best = v[u];
                 bi = j0 + u * kArgThreads;
