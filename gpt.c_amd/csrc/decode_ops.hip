@@ -52,7 +52,11 @@ struct RowsArgs {
 template <bool kVec, bool kLN, int kOuts, int kPer>
 __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a) {
     constexpr int kSplit = kWaves / kOuts;
-    constexpr int kIt = 4;  // 16-byte steps per lane loaded up front (in_f <= 1024 kSplit)
+    // 16-byte steps per lane loaded up front (in_f <= 1024 kSplit).  Wide
+    // outputs (kPer > 1: the vocabulary projection, bandwidth-bound) stream
+    // instead: their registers buy occupancy there (34 against 40 us).
+    constexpr int kIt = kPer == 1 ? 4 : 0;
+    constexpr int kItN = kIt > 0 ? kIt : 1;
     __shared__ float part[kWaves * kPer][kMaxRows];
     __shared__ float stat[2][kMaxRows];
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
@@ -75,7 +79,7 @@ __global__ __launch_bounds__(kThreads) void linear_rows_kernel(const RowsArgs a)
     }
     // kVec: the wave's first kIt weight vectors per output (and LayerNorm vectors).
     const int jb = j0 / 4 + lane, je = j1 / 4;
-    f32x4_t wv[kIt][kPer], lw[kIt], lb[kIt];
+    f32x4_t wv[kItN][kPer], lw[kItN], lb[kItN];
     if (kVec && o0 < a.out_f) {
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
