@@ -709,8 +709,11 @@ def attention_bench(args):
         # Kernel symbols per head size (D == 64: the 16-row kernels; short
         # heads: T <= 64 one workgroup per block, 64 < T <= 128 two per head).
         fwd_sym = "attn_fwd16_kernel" if T > 128 else ("attn_fwd_twotile_kernel" if T > 64 else "attn_fwd_short_kernel")
+        # dk/dv: the LDS-direct kernel for D == 64 heads with the stored P'
+        # (T > 128), the general one otherwise.
         symbols = {"fwd": "attn_fwd_kernel" if D != 64 else fwd_sym,
-                   "bwd_delta": "attn_bwd_delta_kernel", "bwd_dkdv": "attn_bwd_dkdv_kernel",
+                   "bwd_delta": "attn_bwd_delta_kernel",
+                   "bwd_dkdv": "attn_bwd_dkdv_dma_kernel" if D == 64 and T > 128 else "attn_bwd_dkdv_kernel",
                    "bwd_dq": "attn_bwd_dq16_kernel" if D == 64 else "attn_bwd_dq_kernel"}
         dom = "fwd" if fwd_only else max(k_ms, key=k_ms.get)
         if fwd_only:
@@ -723,13 +726,24 @@ def attention_bench(args):
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                     "algorithmic_bytes_per_launch": fwd_bytes}
         else:
-            dur_ms, dur_src = k_ms[dom], "median of the per-kernel event pass"
+            # The per-kernel pass brackets every launch with events, which adds
+            # a fixed cost to each interval that the headline pass (no events)
+            # does not pay: the four medians sum to more than ms_step.  That
+            # excess, shared equally, is taken off the dominant kernel's median
+            # (a kernel trace of the headline pass gives the same duration).
+            ev_ms = k_ms[dom]
+            per_event = max(0.0, (sum(k_ms.values()) - ms_step) / len(k_ms))
+            dur_ms = ev_ms - per_event
+            dur_src = ("median of the per-kernel event pass less the events' cost: (sum of the per-kernel medians "
+                       "- headline ms/step) / number of kernels")
             achieved = kernel_flops[dom] / (dur_ms * 1e-3) / 1e12
             roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": round(peak, 2),
                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
                     "algorithmic_flop_per_launch": kernel_flops[dom]}
         roof["duration_ms"] = round(dur_ms, 5)
         roof["duration_source"] = dur_src
+        if not fwd_only:
+            roof["duration_event_ms"] = round(ev_ms, 5)
         # HBM bytes per launch from the committed rocprof byte-counter runs
         # (FETCH_SIZE and WRITE_SIZE, scaled by a plain copy of known size).
         traffic_file = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.config}.json")
