@@ -418,7 +418,10 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 // s_waitcnt vmcnt(0) (through the builtin, so that the compiler's own
 // counting knows every earlier load has landed) right before that barrier.
 // Loads the compiler issues later are younger than the tile's, so its own
-// waits can only over-wait, never under-wait.
+// waits can only over-wait, never under-wait.  The asm sets M0 (the LDS
+// address of the row) before each load; the compiler ignores an M0 clobber,
+// and its code for this kernel uses M0 nowhere else (gfx950's DS
+// instructions do not read it; checked in the generated code).
 //
 // BIAS: the q bias is added to the Q operand of dK += dS^T Q as it is read
 // (the same sum as adding it to the stored tile: rows past T then hold the
