@@ -252,17 +252,18 @@ attn_fwd_kernel(const FwdParams a) {
 // with lazy rescaling (the running maximum moves only when a row maximum
 // grows by more than 2^kRescaleLog2), P' = exp2(S c2 - m_use) into sc and its
 // row sums into l_run.  Returns m_use (0 while the row is all masked).
-template <int NKB, bool DIAG>
-__device__ __forceinline__ float fwd16_scores(const float *k_t, const f32x4 (&qr)[4], int g, int i16, float c2,
-                                              float &m_run, float &l_run, f32x4 (&acc)[4], f32x4 (&sc)[4]) {
+// The K operands come from k_op(kb, c): K[16kb + i16][16g + 4c .. +3] of the
+// tile (an LDS read, or registers the caller loaded).
+template <int NKB, bool DIAG, typename KOp>
+__device__ __forceinline__ float fwd16_scores_op(KOp k_op, const f32x4 (&qr)[4], int g, int i16, float c2,
+                                                 float &m_run, float &l_run, f32x4 (&acc)[4], f32x4 (&sc)[4]) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) sc[kb] = zero4();
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         f32x4 ka[NKB];
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-            ka[kb] = *reinterpret_cast<const f32x4 *>(&k_t[(16 * kb + i16) * kLdsStride + 16 * g + 4 * c]);
+        for (int kb = 0; kb < NKB; ++kb) ka[kb] = k_op(kb, c);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -302,19 +303,39 @@ __device__ __forceinline__ float fwd16_scores(const float *k_t, const f32x4 (&qr
     return m_use;
 }
 
+template <int NKB, bool DIAG>
+__device__ __forceinline__ float fwd16_scores(const float *k_t, const f32x4 (&qr)[4], int g, int i16, float c2,
+                                              float &m_run, float &l_run, f32x4 (&acc)[4], f32x4 (&sc)[4]) {
+    return fwd16_scores_op<NKB, DIAG>(
+        [&](int kb, int c) {
+            return *reinterpret_cast<const f32x4 *>(&k_t[(16 * kb + i16) * kLdsStride + 16 * g + 4 * c]);
+        },
+        qr, g, i16, c2, m_run, l_run, acc, sc);
+}
+
 // O^T += V^T P^T: step (kb, r) reduces keys 16kb + 4g' + r; lane i16's A
 // operands for the four dim blocks are V[key][4 i16 .. 4 i16 + 3] (one
 // 16-byte LDS read), and acc[db][r] = O[my_q][16g + 4r + db].
-template <int NKB>
-__device__ __forceinline__ void fwd16_pv(const float *v_t, const f32x4 (&sc)[4], int g, int i16, f32x4 (&acc)[4]) {
+// The V operands come from v_op(kb, r): V[16kb + 4g + r][4 i16 .. +3].
+template <int NKB, typename VOp>
+__device__ __forceinline__ void fwd16_pv_op(VOp v_op, const f32x4 (&sc)[4], f32x4 (&acc)[4]) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const f32x4 va = *reinterpret_cast<const f32x4 *>(&v_t[(16 * kb + 4 * g + r) * kLdsStride + 4 * i16]);
+            const f32x4 va = v_op(kb, r);
 #pragma unroll
             for (int db = 0; db < 4; ++db) acc[db] = mfma16(va[db], sc[kb][r], acc[db]);
         }
+}
+
+template <int NKB>
+__device__ __forceinline__ void fwd16_pv(const float *v_t, const f32x4 (&sc)[4], int g, int i16, f32x4 (&acc)[4]) {
+    fwd16_pv_op<NKB>(
+        [&](int kb, int r) {
+            return *reinterpret_cast<const f32x4 *>(&v_t[(16 * kb + 4 * g + r) * kLdsStride + 4 * i16]);
+        },
+        sc, acc);
 }
 
 // ---- The 16-row forward (D == 64, buffer-resource loads) ----
@@ -680,14 +701,15 @@ attn_fwd_short_kernel(const FwdParams a) {
 // block's 1 .. 4.  Four workgroups per head, each one long and one short
 // slab (9 units), and every slab cut into pieces of at most 3 consecutive
 // key blocks, one piece per wave: no wave carries more than 3 units (96
-// MFMAs).  The pieces of a slab merge their partial softmax states (running
-// max, sums, O) through LDS after the workgroup's one barrier of the compute
-// phase, in a fixed order.
+// MFMAs).  A wave loads the K and V rows of its piece straight into the
+// registers it uses them from (no staging through LDS, no barrier before
+// the compute), and the pieces of a slab merge their partial softmax states
+// (running max, sums, O) through LDS after the workgroup's one barrier, in
+// a fixed order.
 //   role 0: slabs (1,3) [blocks 0-2 | 3-5 | 6-7] and (0,0) [0]
 //   role 1: slabs (1,2) [0-2 | 3-5 | 6] and (0,1) [0-1]
 //   role 2: slabs (1,1) [0-2 | 3-5] and (0,2) [0-2]
 //   role 3: slabs (1,0) [0-2 | 3-4] and (0,3) [0-1 | 2-3]
-// Every workgroup stages the head's two K/V tiles (key k in LDS row k).
 struct SlabState {
     float m_run, l_run;
     f32x4 acc[4];
@@ -697,9 +719,6 @@ constexpr int kTwoTileRoles = 4;  // workgroups per head
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 attn_fwd_twotile_kernel(const FwdParams a) {
-    constexpr int TILE = kFwdBN * kLdsStride;
-    __shared__ __attribute__((aligned(16))) float k_lds[2 * TILE];
-    __shared__ __attribute__((aligned(16))) float v_lds[2 * TILE];
     __shared__ __attribute__((aligned(16))) f32x4 part_lds[2][5][64];  // [partial][acc0..3, {m, l}][lane]
 
     const int tid = threadIdx.x;
@@ -717,47 +736,19 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     const int job = 4 * role + w;  // wave-uniform
     constexpr int kJobSlab[16][2] = {{1, 3}, {1, 3}, {1, 3}, {0, 0}, {1, 2}, {1, 2}, {1, 2}, {0, 1},
                                      {1, 1}, {1, 1}, {0, 2}, {-1, 0}, {1, 0}, {1, 0}, {0, 3}, {0, 3}};
-    const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
-    f32x4 kpre[2][4], vpre[2][4];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t key = kt * kFwdBN + ld_row + 16 * i;
-            kpre[kt][i] = buffer_load4(k_rows, key * a.k.st + ld_col);
-            vpre[kt][i] = buffer_load4(v_rows, key * a.v.st + ld_col);
-        }
+    const int sj = kJobSlab[job][0], ss = kJobSlab[job][1];
     // The qkv bias: key rows past T then hold the bias; they are masked for
     // every query < T, and rows of queries past T are not written.
     const bool biased = a.kb != nullptr;
-    f32x4 kb4 = zero4(), vb4 = zero4(), qb4[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qb4[c] = zero4();
-    if (biased) {
-        kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + ld_col);
-        vb4 = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + ld_col);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qb4[c] = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * g + 4 * c);
-    }
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = ld_row + 16 * i;
-            *reinterpret_cast<f32x4 *>(&k_lds[kt * TILE + row * kLdsStride + ld_col]) = kpre[kt][i] + kb4;
-            *reinterpret_cast<f32x4 *>(&v_lds[kt * TILE + row * kLdsStride + ld_col]) = vpre[kt][i] + vb4;
-        }
-    // The Q rows of the wave's slab, with the q bias (issued after the K/V
-    // loads: issuing them first measured no faster, warm or cold).
-    const int sj = kJobSlab[job][0], ss = kJobSlab[job][1];
     f32x4 qr[4];
     if (sj >= 0) {
         const int q = sj * kF16Rows + 16 * ss + i16;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c) + qb4[c];
+        for (int c = 0; c < 4; ++c) {
+            qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c);
+            if (biased) qr[c] += *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * g + 4 * c);
+        }
     }
-    __syncthreads();
 
     const float c2 = a.scale_log2;
     SlabState st;
@@ -767,12 +758,35 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     for (int db = 0; db < 4; ++db) st.acc[db] = zero4();
     f32x4 sc[4];
     // Key blocks KB0 .. KB0 + NKB - 1 of the wave's slab (DIAG: the last is the
-    // slab's diagonal block, masked per key).
+    // slab's diagonal block, masked per key), their K and V rows loaded here:
+    // kr[kb][c] = K[16(KB0 + kb) + i16][16g + 4c ..], vr[kb][r] = V[16(KB0 + kb) + 4g + r][4 i16 ..].
     auto piece = [&](auto kb0_c, auto nkb_c, auto diag_c) {
         constexpr int KB0 = decltype(kb0_c)::value, NKB = decltype(nkb_c)::value;
         constexpr bool DIAG = decltype(diag_c)::value;
-        fwd16_scores<NKB, DIAG>(k_lds + 16 * KB0 * kLdsStride, qr, g, i16, c2, st.m_run, st.l_run, st.acc, sc);
-        fwd16_pv<NKB>(v_lds + 16 * KB0 * kLdsStride, sc, g, i16, st.acc);
+        f32x4 kr[NKB][4], vr[NKB][4];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t kk = 16 * (KB0 + kb) + i16, vk = 16 * (KB0 + kb) + 4 * g + c;
+                kr[kb][c] = buffer_load4(k_rows, kk * a.k.st + 16 * g + 4 * c);
+                vr[kb][c] = buffer_load4(v_rows, vk * a.v.st + 4 * i16);
+            }
+        if (biased) {
+            const f32x4 vb4 = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 4 * i16);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f32x4 kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + 16 * g + 4 * c);
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    kr[kb][c] += kb4;
+                    vr[kb][c] += vb4;
+                }
+            }
+        }
+        fwd16_scores_op<NKB, DIAG>([&](int kb, int c) { return kr[kb][c]; }, qr, g, i16, c2, st.m_run, st.l_run,
+                                   st.acc, sc);
+        fwd16_pv_op<NKB>([&](int kb, int r) { return vr[kb][r]; }, sc, st.acc);
     };
     auto finish = [&]() {
         const int my_q = sj * kF16Rows + 16 * ss + i16;
