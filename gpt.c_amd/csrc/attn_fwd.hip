@@ -745,8 +745,8 @@ attn_fwd_twotile_kernel(const FwdParams a) {
         const int q = sj * kF16Rows + 16 * ss + i16;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c);
-            if (biased) qr[c] += *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * g + 4 * c);
+            qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * c + 4 * g);
+            if (biased) qr[c] += *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * c + 4 * g);
         }
     }
 
@@ -759,7 +759,10 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     f32x4 sc[4];
     // Key blocks KB0 .. KB0 + NKB - 1 of the wave's slab (DIAG: the last is the
     // slab's diagonal block, masked per key), their K and V rows loaded here:
-    // kr[kb][c] = K[16(KB0 + kb) + i16][16g + 4c ..], vr[kb][r] = V[16(KB0 + kb) + 4g + r][4 i16 ..].
+    // kr[kb][c] = K[16(KB0 + kb) + i16][16c + 4g ..], vr[kb][r] = V[16(KB0 + kb) + 4g + r][4 i16 ..].
+    // Step (c, e) of the scores reduces dim 16c + 4g + e on lane group g (Q
+    // likewise): any one-to-one map of the dims gives the same products, and
+    // this one makes each K load 64 contiguous bytes of a row per lane group.
     auto piece = [&](auto kb0_c, auto nkb_c, auto diag_c) {
         constexpr int KB0 = decltype(kb0_c)::value, NKB = decltype(nkb_c)::value;
         constexpr bool DIAG = decltype(diag_c)::value;
@@ -769,14 +772,14 @@ attn_fwd_twotile_kernel(const FwdParams a) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const uint32_t kk = 16 * (KB0 + kb) + i16, vk = 16 * (KB0 + kb) + 4 * g + c;
-                kr[kb][c] = buffer_load4(k_rows, kk * a.k.st + 16 * g + 4 * c);
+                kr[kb][c] = buffer_load4(k_rows, kk * a.k.st + 16 * c + 4 * g);
                 vr[kb][c] = buffer_load4(v_rows, vk * a.v.st + 4 * i16);
             }
         if (biased) {
             const f32x4 vb4 = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 4 * i16);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const f32x4 kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + 16 * g + 4 * c);
+                const f32x4 kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + 16 * c + 4 * g);
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
                     kr[kb][c] += kb4;
