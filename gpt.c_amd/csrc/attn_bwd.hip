@@ -408,11 +408,18 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 // ---- dK, dV of D == 64 heads with the stored P' (the long-head path) ----
 // The same per-wave work as attn_bwd_dkdv_kernel<true, true, false>, with the
 // Q and dO tiles double-buffered in LDS and filled by buffer loads that write
-// LDS directly (one row of 64 floats per instruction, lanes -> consecutive
-// dims; rows past T read as zeros through the buffer resource).  Tile qt + 1
-// is requested right after the barrier that opens tile qt, so one barrier per
-// tile both publishes the next tile and frees the previous one, and the tile
-// loads take no registers and no LDS store instructions.
+// LDS directly (64 floats per instruction; rows past T read as zeros through
+// the buffer resource).  Tile qt + 1 is requested right after the barrier that
+// opens tile qt, so one barrier per tile both publishes the next tile and
+// frees the previous one, and the tile loads take no registers and no LDS
+// store instructions.
+//
+// dO is stored by rows (one row per instruction): dP = dO V^T reads a lane's
+// query row as float4s.  Q feeds only dK += dS^T Q, whose B operand gives a
+// lane one dim of 4 consecutive queries per 4 MFMAs, so Q is stored as
+// [query / 4][dim][query % 4]: one 16-byte read per lane and 4 MFMAs.  Each
+// load instruction gathers 16 dims of 4 consecutive rows (4 pieces of 64
+// bytes) into 64 consecutive LDS words.
 //
 // The compiler does not see these loads: the wait for them is an explicit
 // s_waitcnt vmcnt(0) (through the builtin, so that the compiler's own
@@ -431,8 +438,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 attn_bwd_dkdv_dma_kernel(const BwdParams a) {
     constexpr int LS = kDPad + 4;      // LDS row stride (floats)
     constexpr int NJ = kDPad / 8;      // reduction steps of 8 dims (4 per lane half)
-    constexpr int kTile = kBwdBQ * LS;  // floats per LDS tile
-    __shared__ __attribute__((aligned(16))) float q_lds[2 * kTile];
+    constexpr int kTile = kBwdBQ * LS;      // floats per dO tile (rows)
+    constexpr int kQTile = kBwdBQ * kDPad;  // floats per Q tile ([q / 4][dim][q % 4])
+    __shared__ __attribute__((aligned(16))) float q_lds[2 * kQTile];
     __shared__ __attribute__((aligned(16))) float do_lds[2 * kTile];
     // Per buffer, one entry per thread: [0, 128) the factors f of P = P' * f
     // for the workgroup's two 64-key tiles ([key tile][query]), [128, 192)
@@ -491,20 +499,27 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
     const auto q_rows = head_rows(Qh, T, a.q.st);
     const auto do_rows = head_rows(dOh, T, a.dout.st);
 
-    // Rows 16w .. 16w+15 of tile qt into LDS buffer buf (M0 = the row's LDS byte address).
+    // Rows 16w .. 16w+15 of tile qt into LDS buffer buf (M0 = the LDS byte
+    // address the instruction's 64 words start at).  dO: row q0 + i, lane ->
+    // dim.  Q: instruction i takes rows q0 + 4(i/4) + (lane % 4), dims
+    // 16(i % 4) + lane / 4, i.e. group q4 = 4w + i/4 of the tile, words
+    // [64(i % 4), 64(i % 4) + 64) of the group's 256.
     const uint32_t vl = 4u * lane;
+    const uint32_t vq = 4u * ((lane & 3) * a.q.st + (lane >> 2));
     const uint32_t lds_q = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-                               (__attribute__((address_space(3))) float *)q_lds)) + 16u * w * LS * 4u);
+                               (__attribute__((address_space(3))) float *)q_lds)) + 16u * w * kDPad * 4u);
     const uint32_t lds_do = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
                                 (__attribute__((address_space(3))) float *)do_lds)) + 16u * w * LS * 4u);
     auto load_tile = [&](int qt, int buf) {
         const uint32_t q0 = static_cast<uint32_t>(qt * kBwdBQ + 16 * w);
-        const uint32_t mq = lds_q + buf * (kTile * 4u), md = lds_do + buf * (kTile * 4u);
+        const uint32_t mq = lds_q + buf * (kQTile * 4u), md = lds_do + buf * (kTile * 4u);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint32_t q = q0 + i;
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(mq + i * LS * 4u),
-                         "v"(q * a.q.st * 4u + vl), "s"(q_rows)
+            const uint32_t gq = q0 + 4 * (i >> 2);
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(
+                             mq + (i >> 2) * (4u * kDPad * 4u) + (i & 3) * 256u),
+                         "v"(gq * a.q.st * 4u + (i & 3) * 64u + vq), "s"(q_rows)
                          : "memory");
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(md + i * LS * 4u),
                          "v"(q * a.dout.st * 4u + vl), "s"(do_rows)
@@ -560,7 +575,7 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         __syncthreads();
         if (qt + 1 < q_end) load_tile(qt + 1, buf ^ 1);
 
-        const float *qs = q_lds + buf * kTile, *dos = do_lds + buf * kTile;
+        const float *qs = q_lds + buf * kQTile, *dos = do_lds + buf * kTile;
         const float *f_w = stat_lds + buf * 256 + (w >> 1) * kBwdBQ;
         const float *dl_w = stat_lds + buf * 256 + 2 * kBwdBQ;
 #pragma unroll
@@ -601,17 +616,24 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
                 for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
             }
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
+            for (int g = 0; g < 4; ++g) {
+                // Q rows 32qb + 8g + 4hf + c, c = 0..3, dim 32db + l32.
+                f32x4 q4[2];
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+                    q4[db] = *reinterpret_cast<const f32x4 *>(&qs[(8 * qb + 2 * g + hf) * (4 * kDPad) +
+                                                                   (32 * db + l32) * 4]);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int row = 32 * qb + 8 * g + 4 * hf + c;
 #pragma unroll
                     for (int db = 0; db < 2; ++db) {
-                        const float qv = qs[row * LS + 32 * db + l32];
+                        const float qv = q4[db][c];
                         acc_dv[db] = mfma32(s[4 * g + c], dos[row * LS + 32 * db + l32], acc_dv[db]);
                         acc_dk[db] = mfma32(dp[4 * g + c], BIAS ? qv + qbias[db] : qv, acc_dk[db]);
                     }
                 }
+            }
         }
     }
 
