@@ -365,7 +365,7 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
                 "The forward kept the log-sum-exp-only state, which only the D = 64 kernels read, but these "
                 "gradient buffers need the other kernels (unaligned rows).");
     hipStream_t s = gptc_stream_checked();
-    gptc::bwd_split_plan(p);
+    gptc::bwd_split_plan(p, s);
     bool folded = false;
     if (bias != nullptr) {
         CHECK_ERROR(!compact, "The qkv bias can be folded in with the compact cache layout only.");

@@ -406,13 +406,20 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 }
 
 // ---- dK, dV of D == 64 heads with the stored P' (the long-head path) ----
-// The same per-wave work as attn_bwd_dkdv_kernel<true, true, false>, with the
-// Q and dO tiles double-buffered in LDS and filled by buffer loads that write
-// LDS directly (64 floats per instruction; rows past T read as zeros through
-// the buffer resource).  Tile qt + 1 is requested right after the barrier that
-// opens tile qt, so one barrier per tile both publishes the next tile and
-// frees the previous one, and the tile loads take no registers and no LDS
-// store instructions.
+// The same per-wave work as attn_bwd_dkdv_kernel<true, true, false> on one
+// 128-key block (wave w: keys 32w .. 32w+31 of it), run over work lists
+// (block_sched.hpp): each workgroup takes its items (query tiles [qa, qe) of
+// key block kb of head bh) one after the other, as one sequence of steps
+// (one step = one 64-query tile of one item).
+//
+// The Q and dO tiles are double-buffered in LDS and filled by buffer loads
+// that write LDS directly (64 floats per instruction; rows past T read as
+// zeros through the buffer resource).  The tile of the next step (the next
+// item's first one at the end of an item) is requested right after the
+// barrier that opens a step, so one barrier per step both publishes the next
+// tile and frees the previous one, and the tile loads take no registers and
+// no LDS store instructions.  The statistics and the P' rows of the next step
+// are loaded during this one likewise.
 //
 // dO is stored by rows (one row per instruction): dP = dO V^T reads a lane's
 // query row as float4s.  Q feeds only dK += dS^T Q, whose B operand gives a
@@ -430,9 +437,12 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 // and its code for this kernel uses M0 nowhere else (gfx950's DS
 // instructions do not read it; checked in the generated code).
 //
-// BIAS: the q bias is added to the Q operand of dK += dS^T Q as it is read
-// (the same sum as adding it to the stored tile: rows past T then hold the
-// bias, with dS = 0 there).
+// At the end of an item its dK, dV rows are stored (added, for the two items
+// of a key block kb < nsplit), then the next item's V rows are loaded.
+//
+// BIAS: the v bias joins the V rows as they are loaded; the q bias is added
+// to the Q operand of dK += dS^T Q as it is read (the same sum as adding it
+// to the stored tile: rows past T then hold the bias, with dS = 0 there).
 template <bool BIAS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 attn_bwd_dkdv_dma_kernel(const BwdParams a) {
@@ -451,57 +461,60 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
-    const int bh = blockIdx.x % a.bh_pad;
-    if (bh >= a.B * a.H) return;
-    const int row_idx = static_cast<int>(blockIdx.x / a.bh_pad);
-    const int slot = a.nsplit > 0 ? a.slot[row_idx] : 2 * row_idx;
-    const int kb_idx = slot >> 1, part = slot & 1;
-    const bool split = kb_idx < a.nsplit;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int T = a.T;
+    const int it_end = a.ksched.wg_start[blockIdx.x + 1];
+    const int it0 = a.ksched.wg_start[blockIdx.x];
+    if (it0 >= it_end) return;
+    const int T = a.T, n_qt = a.nqt;
 
-    const int k_blk0 = kb_idx * kBwdBK;
-    const int kw0 = k_blk0 + 32 * w;
-    const int my_k = kw0 + l32;
-    const bool k_ok = my_k < T;
-
-    const float *Qh = a.q.p + b * a.q.sb + h * a.q.sh;
-    const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
-    const float *dOh = a.dout.p + b * a.dout.sb + h * a.dout.sh;
-    const float *lse_h = a.lse + static_cast<uint32_t>(bh) * T;
-    const float *dl_h = a.delta + static_cast<uint32_t>(bh) * T;
-    const float *pm_h = a.pm + static_cast<uint32_t>(bh) * a.nqt * T;
+    // A step: tile qt of item it = (bh, kb, qa, qe).  All fields are uniform.
+    struct Step {
+        int it, bh, kb, qa, qt, qe;
+    };
+    auto item_step = [&](int i) {
+        const int *e = a.ksched.items + 4 * i;
+        return Step{i, e[0], e[1], e[2], e[2], e[3]};
+    };
+    // The step after s: the next tile of its item, or the next item's first.
+    auto advance = [&](Step &s) {
+        if (s.qt + 1 < s.qe) {
+            ++s.qt;
+            return true;
+        }
+        if (s.it + 1 >= it_end) return false;
+        s = item_step(s.it + 1);
+        return true;
+    };
+    auto head_of = [&](int bh, int &b, int &h) {
+        b = bh / a.H;
+        h = bh - b * a.H;
+    };
 
     // V row of this lane's key, dims 8j + 4hf + c: B operand of dP = dO V^T.
+    // BIAS: the v bias joins it (keys past T keep a zero row); qbias holds
+    // the q bias of this lane's two dims.
     f32x4 vr[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) vr[j] = k_ok ? load4<true>(Vh + my_k * a.v.st, 8 * j + 4 * hf, kDPad) : zero4();
-    // BIAS: the v bias joins this key's V row (keys past T keep a zero row);
-    // the q bias of this lane's two dims joins the Q operand below.
-    f32x4 vbias[NJ];
     float qbias[2] = {0.0f, 0.0f};
-    if (BIAS) {
+    auto load_v = [&](const Step &s) {
+        int b, h;
+        head_of(s.bh, b, h);
+        const int my_k = s.kb * kBwdBK + 32 * w + l32;
+        const bool k_ok = my_k < T;
+        const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) vbias[j] = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 8 * j + 4 * hf);
-        qbias[0] = a.qb[h * kDPad + l32];
-        qbias[1] = a.qb[h * kDPad + 32 + l32];
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    if (BIAS && k_ok) {
+        for (int j = 0; j < NJ; ++j) vr[j] = k_ok ? load4<true>(Vh + my_k * a.v.st, 8 * j + 4 * hf, kDPad) : zero4();
+        if (BIAS) {
+            if (k_ok) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) vr[j] += vbias[j];
-    }
+                for (int j = 0; j < NJ; ++j) vr[j] += *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 8 * j + 4 * hf);
+            }
+            qbias[0] = a.qb[h * kDPad + l32];
+            qbias[1] = a.qb[h * kDPad + 32 + l32];
+        }
+    };
 
-    const int n_qt = a.nqt;
-    const int qt_diag = k_blk0 / kBwdBQ, q_mid = qt_diag + (n_qt - qt_diag + 1) / 2;
-    const int qt0 = split && part ? q_mid : qt_diag;
-    const int q_end = split && !part ? q_mid : n_qt;
-    const auto q_rows = head_rows(Qh, T, a.q.st);
-    const auto do_rows = head_rows(dOh, T, a.dout.st);
-
-    // Rows 16w .. 16w+15 of tile qt into LDS buffer buf (M0 = the LDS byte
-    // address the instruction's 64 words start at).  dO: row q0 + i, lane ->
-    // dim.  Q: instruction i takes rows q0 + 4(i/4) + (lane % 4), dims
+    // Rows 16w .. 16w+15 of the step's tile into LDS buffer buf (M0 = the LDS
+    // byte address the instruction's 64 words start at).  dO: row q0 + i,
+    // lane -> dim.  Q: instruction i takes rows q0 + 4(i/4) + (lane % 4), dims
     // 16(i % 4) + lane / 4, i.e. group q4 = 4w + i/4 of the tile, words
     // [64(i % 4), 64(i % 4) + 64) of the group's 256.
     const uint32_t vl = 4u * lane;
@@ -510,8 +523,12 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
                                (__attribute__((address_space(3))) float *)q_lds)) + 16u * w * kDPad * 4u);
     const uint32_t lds_do = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
                                 (__attribute__((address_space(3))) float *)do_lds)) + 16u * w * LS * 4u);
-    auto load_tile = [&](int qt, int buf) {
-        const uint32_t q0 = static_cast<uint32_t>(qt * kBwdBQ + 16 * w);
+    auto load_tile = [&](const Step &s, int buf) {
+        int b, h;
+        head_of(s.bh, b, h);
+        const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
+        const auto do_rows = head_rows(a.dout.p + b * a.dout.sb + h * a.dout.sh, T, a.dout.st);
+        const uint32_t q0 = static_cast<uint32_t>(s.qt * kBwdBQ + 16 * w);
         const uint32_t mq = lds_q + buf * (kQTile * 4u), md = lds_do + buf * (kTile * 4u);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -526,61 +543,135 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
                          : "memory");
         }
     };
-    // The statistics of a tile, loaded one tile ahead (see attn_bwd_dkdv_kernel).
+    // The statistics of a step, loaded one step ahead (see attn_bwd_dkdv_kernel).
     float st0 = 0.0f, st1 = 0.0f;
     bool st_ok = false;
-    auto load_stats = [&](int qt) {
-        const int q = qt * kBwdBQ + (tid & (kBwdBQ - 1));
+    auto load_stats = [&](const Step &s) {
+        const uint32_t bh = static_cast<uint32_t>(s.bh);
+        const int q = s.qt * kBwdBQ + (tid & (kBwdBQ - 1));
         const int qc = min(q, T - 1);
         const bool is_m = tid < 2 * kBwdBQ;
-        const int kt = 2 * kb_idx + ((tid >> 6) & 1);
+        const int kt = 2 * s.kb + ((tid >> 6) & 1);
         st_ok = q < T && (!is_m || kt < n_qt);
-        st0 = *(is_m ? pm_h + min(kt, n_qt - 1) * T + qc : dl_h + qc);
-        st1 = lse_h[qc];
+        st0 = *(is_m ? a.pm + bh * n_qt * T + min(kt, n_qt - 1) * T + qc : a.delta + bh * T + qc);
+        st1 = a.lse[bh * T + qc];
     };
 
     float pbuf[16];
-    auto half_needed = [&](int qt, int qb) {
-        const int qh0 = qt * kBwdBQ + 32 * qb;
+    auto half_needed = [&](const Step &s, int qb) {
+        const int qh0 = s.qt * kBwdBQ + 32 * qb, kw0 = s.kb * kBwdBK + 32 * w;
         return qh0 + 31 >= kw0 && kw0 < T && qh0 < T;
     };
     const uint32_t lane_off = 4 * hf * 32 + l32;
-    auto half_base = [&](int qt, int qb) {
-        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh, n_qt, qt, kw0 >> 5)) + 32 * qb * 32);
+    auto half_base = [&](const Step &s, int qb) {
+        const int kw0 = s.kb * kBwdBK + 32 * w;
+        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(s.bh, n_qt, s.qt, kw0 >> 5)) + 32 * qb * 32);
     };
-    auto load_p = [&](int qt, int qb) {
-        if (!half_needed(qt, qb)) return;
-        const float *hb = half_base(qt, qb);
+    auto load_p = [&](const Step &s, int qb) {
+        if (!half_needed(s, qb)) return;
+        const float *hb = half_base(s, qb);
 #pragma unroll
         for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
     };
-    if (qt0 < q_end) {
-        load_tile(qt0, 0);
-        load_stats(qt0);
-        load_p(qt0, 0);
-    }
 
     f32x16 acc_dk[2], acc_dv[2];
 #pragma unroll
     for (int db = 0; db < 2; ++db) acc_dk[db] = acc_dv[db] = zero16();
 
-    for (int qt = qt0, buf = 0; qt < q_end; ++qt, buf ^= 1) {
+    // Accumulator layout (keys x dims): lane -> dim 32*db + l32,
+    // register r -> key kw0 + 8(r/4) + 4hf + r%4.
+    auto finish_item = [&](const Step &s) {
+        int b, h;
+        head_of(s.bh, b, h);
+        const int kw0 = s.kb * kBwdBK + 32 * w;
+        const bool split = s.kb < a.nsplit;
+        float *dKh = a.dk.p + b * a.dk.sb + h * a.dk.sh;
+        float *dVh = a.dv.p + b * a.dv.sb + h * a.dv.sh;
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+            const int dim = 32 * db + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+                if (key < T) {
+                    if (split) {
+                        unsafeAtomicAdd(&dKh[key * a.dk.st + dim], acc_dk[db][r] * a.scale);
+                        unsafeAtomicAdd(&dVh[key * a.dv.st + dim], acc_dv[db][r]);
+                    } else {
+                        dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
+                        dVh[key * a.dv.st + dim] = acc_dv[db][r];
+                    }
+                }
+            }
+        }
+        if (a.db != nullptr) {
+            // db of the k and v parts, as in attn_bwd_dkdv_kernel.  red_lds is
+            // free: its last readers passed at least one step barrier since.
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                float sk = 0.0f, sv = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const bool ok = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3) < T;
+                    sk += ok ? acc_dk[db][r] : 0.0f;
+                    sv += ok ? acc_dv[db][r] : 0.0f;
+                }
+                sk += other_half(sk);
+                sv += other_half(sv);
+                if (hf == 0) {
+                    red_lds[w][32 * db + l32] = sk * a.scale;
+                    red_lds[w][kDPad + 32 * db + l32] = sv;
+                }
+            }
+            __syncthreads();
+            if (tid < 2 * kDPad) {
+                const float sum = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
+                const int col = (tid < kDPad ? 0 : a.C) + h * kDPad + (tid & (kDPad - 1));
+                const int prow = split && s.qa != 2 * s.kb ? a.nkb + s.kb : s.kb;
+                a.dbkv_part[(static_cast<size_t>(b) * (a.nkb + a.nsplit) + prow) * 2 * a.C + col] = sum;
+            }
+        }
+    };
+
+    Step cur = item_step(it0);
+    load_v(cur);
+    load_tile(cur, 0);
+    load_stats(cur);
+    load_p(cur, 0);
+    int total_steps = 0, done_steps = 0;
+    for (int i = it0; i < it_end; ++i) total_steps += a.ksched.items[4 * i + 3] - a.ksched.items[4 * i + 2];
+
+    for (int buf = 0;; buf ^= 1) {
+        // Wave priority from the share of the list still to run (4 levels):
+        // the SIMDs otherwise issue from the oldest waves first, so the CU's
+        // first workgroup runs ahead and the other one runs alone at the end;
+        // a workgroup that falls behind now wins the MFMA pipe and catches up.
+        switch ((4 * (total_steps - done_steps)) / (total_steps + 1)) {  // wave-uniform
+            case 0: __builtin_amdgcn_s_setprio(0); break;
+            case 1: __builtin_amdgcn_s_setprio(1); break;
+            case 2: __builtin_amdgcn_s_setprio(2); break;
+            default: __builtin_amdgcn_s_setprio(3); break;
+        }
+        ++done_steps;
         {
             const float f = fast_exp2(st0 - st1 * kLog2e);
             stat_lds[buf * 256 + tid] = st_ok ? (tid < 2 * kBwdBQ ? f : st0) : 0.0f;
         }
-        // This wave's loads of tile qt have landed; after the barrier every
-        // wave's have, and tile qt - 1 (the other buffer) is no longer read.
+        // This wave's loads of this step's tile have landed; after the barrier
+        // every wave's have, and the other buffer (the previous step's) is no
+        // longer read.
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
-        if (qt + 1 < q_end) load_tile(qt + 1, buf ^ 1);
+        Step nxt = cur;
+        const bool more = advance(nxt);
+        if (more) load_tile(nxt, buf ^ 1);
 
         const float *qs = q_lds + buf * kQTile, *dos = do_lds + buf * kTile;
         const float *f_w = stat_lds + buf * 256 + (w >> 1) * kBwdBQ;
         const float *dl_w = stat_lds + buf * 256 + 2 * kBwdBQ;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
-            const bool need = half_needed(qt, qb);
+            const bool need = half_needed(cur, qb);
             f32x16 s, dp = zero16();
             if (need) {
 #pragma unroll
@@ -597,10 +688,10 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
                 }
             }
             if (qb == 0) {
-                load_p(qt, 1);
-                if (qt + 1 < q_end) load_stats(qt + 1);
-            } else if (qt + 1 < q_end) {
-                load_p(qt + 1, 0);
+                load_p(cur, 1);
+                if (more) load_stats(nxt);
+            } else if (more) {
+                load_p(nxt, 0);
             }
             if (!need) continue;
 
@@ -611,7 +702,7 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
                 for (int c = 0; c < 4; ++c) dp[4 * g + c] = s[4 * g + c] * (dp[4 * g + c] - d4[c]);  // dS
             }
             {
-                float *hb = half_base(qt, qb);
+                float *hb = half_base(cur, qb);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
             }
@@ -635,54 +726,15 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
                 }
             }
         }
-    }
 
-    // Accumulator layout (keys x dims): lane -> dim 32*db + l32,
-    // register r -> key kw0 + 8(r/4) + 4hf + r%4.
-    float *dKh = a.dk.p + b * a.dk.sb + h * a.dk.sh;
-    float *dVh = a.dv.p + b * a.dv.sb + h * a.dv.sh;
+        if (!more || nxt.it != cur.it) {
+            finish_item(cur);
+            if (!more) break;
+            load_v(nxt);
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
-        const int dim = 32 * db + l32;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-            if (key < T) {
-                if (split) {
-                    unsafeAtomicAdd(&dKh[key * a.dk.st + dim], acc_dk[db][r] * a.scale);
-                    unsafeAtomicAdd(&dVh[key * a.dv.st + dim], acc_dv[db][r]);
-                } else {
-                    dKh[key * a.dk.st + dim] = acc_dk[db][r] * a.scale;
-                    dVh[key * a.dv.st + dim] = acc_dv[db][r];
-                }
-            }
+            for (int db = 0; db < 2; ++db) acc_dk[db] = acc_dv[db] = zero16();
         }
-    }
-    if (a.db != nullptr) {
-        // db of the k and v parts, as in attn_bwd_dkdv_kernel.
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-            float sk = 0.0f, sv = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const bool ok = kw0 + 8 * (r >> 2) + 4 * hf + (r & 3) < T;
-                sk += ok ? acc_dk[db][r] : 0.0f;
-                sv += ok ? acc_dv[db][r] : 0.0f;
-            }
-            sk += other_half(sk);
-            sv += other_half(sv);
-            if (hf == 0) {
-                red_lds[w][32 * db + l32] = sk * a.scale;
-                red_lds[w][kDPad + 32 * db + l32] = sv;
-            }
-        }
-        __syncthreads();
-        if (tid < 2 * kDPad) {
-            const float s = (red_lds[0][tid] + red_lds[1][tid]) + (red_lds[2][tid] + red_lds[3][tid]);
-            const int col = (tid < kDPad ? 0 : a.C) + h * kDPad + (tid & (kDPad - 1));
-            const int prow = split && part ? a.nkb + kb_idx : kb_idx;
-            a.dbkv_part[(static_cast<size_t>(b) * (a.nkb + a.nsplit) + prow) * 2 * a.C + col] = s;
-        }
+        cur = nxt;
     }
 }
 
@@ -1172,64 +1224,16 @@ attn_bwd_dq16_recomp_kernel(const BwdParams a) {
     }
 }
 
-namespace {
-
-// Key blocks are split, longest first, while the grid of key blocks and
-// parts still fits in the GPU's resident workgroup slots: a grid that leaves
-// CUs idle (B * H = 12 heads of T = 1024 make 96 workgroups for 512 slots)
-// is as long as its longest block, and halving the longest blocks halves it
-// (126 -> 70 us measured at B = 1, H = 12, T = 1024).  A grid that fills the
-// slots gains nothing from it (B = 8, H = 12: 204.8 -> 203.2 us with plain
-// stores timed in place of the adds) and would pay for the zeroing and the
-// atomic adds (+6 us), so it is not split.
-std::mutex g_split_mu;
-std::map<int, std::pair<int, int>> g_dkdv_slots;  // device -> (workgroups per CU, CUs)
-
-std::pair<int, int> dkdv_slots() {
-    int dev = 0;
-    hipCheck(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lock(g_split_mu);
-    auto it = g_dkdv_slots.find(dev);
-    if (it == g_dkdv_slots.end()) {
-        int per_cu = 0, cus = 0;
-        hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void *>(attn_bwd_dkdv_dma_kernel<false>), 256, 0));
-        hipCheck(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        it = g_dkdv_slots.emplace(dev, std::make_pair(std::max(1, per_cu), std::max(1, cus))).first;
-    }
-    return it->second;
-}
-
-}  // namespace
-
-int bwd_split_plan(BwdParams &p) {
+int bwd_split_plan(BwdParams &p, hipStream_t stream) {
     p.nsplit = 0;
+    p.k_wg = 0;
+    p.ksched = KeySched{nullptr, nullptr};
     if (!p.full || p.nqt <= kShortHeadTiles || p.ds == nullptr) return 0;  // the recomputing dk/dv runs whole blocks
-    const auto [per_cu, cus] = dkdv_slots();
-    const auto tiles = [&](int kb) { return p.nqt - 2 * kb; };  // query tiles of key block kb
-    const long long slots = static_cast<long long>(per_cu) * cus, bh = static_cast<long long>(p.B) * p.H;
-    int nsplit = 0;
-    while (nsplit < p.nkb && tiles(nsplit) >= 2 && p.nkb + nsplit + 1 <= kBwdMaxSlots &&
-           (p.nkb + nsplit + 1) * bh <= slots)
-        ++nsplit;
-    if (nsplit == 0) return 0;
-    // Grid rows longest first: part 0 of a split block takes the larger half.
-    struct Row {
-        int cost, kb, part;
-    };
-    std::vector<Row> rows;
-    for (int kb = 0; kb < p.nkb; ++kb) {
-        if (kb < nsplit) {
-            rows.push_back({(tiles(kb) + 1) / 2, kb, 0});
-            rows.push_back({tiles(kb) / 2, kb, 1});
-        } else {
-            rows.push_back({tiles(kb), kb, 0});
-        }
-    }
-    std::stable_sort(rows.begin(), rows.end(), [](const Row &x, const Row &y) { return x.cost > y.cost; });
-    for (size_t i = 0; i < rows.size(); ++i) p.slot[i] = static_cast<unsigned short>(2 * rows[i].kb + rows[i].part);
-    p.nsplit = nsplit;
-    return nsplit;
+    // Both instances of the kernel keep two workgroups per CU; the lists are
+    // built for the residency of the one without the bias.
+    p.ksched = device_key_schedule(p.B * p.H, p.nqt, reinterpret_cast<const void *>(attn_bwd_dkdv_dma_kernel<false>),
+                                   stream, &p.k_wg, &p.nsplit);
+    return p.nsplit;
 }
 
 size_t bwd_ds_floats(int B, int H, int T) {
@@ -1254,7 +1258,7 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
     }
     const dim3 block(256);
     const int rows = p.B * p.T * p.H;
-    const dim3 grid_d((rows + 15) / 16), grid_k((p.nkb + p.nsplit) * p.bh_pad), grid_q(p.nqb * p.bh_pad);
+    const dim3 grid_d((rows + 15) / 16), grid_k(p.nkb * p.bh_pad), grid_q(p.nqb * p.bh_pad);
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
     if (p.vec)
         attn_bwd_delta_kernel<true><<<grid_d, block, 0, stream>>>(p);
@@ -1268,9 +1272,9 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
     if (p.full && (p.nqt <= kShortHeadTiles || p.ds == nullptr))
         attn_bwd_dkdv_kernel<true, true, true><<<grid_k, block, 0, stream>>>(p);
     else if (p.full && p.qb != nullptr)
-        attn_bwd_dkdv_dma_kernel<true><<<grid_k, block, 0, stream>>>(p);
+        attn_bwd_dkdv_dma_kernel<true><<<dim3(p.k_wg), block, 0, stream>>>(p);
     else if (p.full)
-        attn_bwd_dkdv_dma_kernel<false><<<grid_k, block, 0, stream>>>(p);
+        attn_bwd_dkdv_dma_kernel<false><<<dim3(p.k_wg), block, 0, stream>>>(p);
     else if (wide && p.vec)
         attn_bwd_dkdv_kernel<true, false, false, 2 * kDPad><<<grid_k, block, 0, stream>>>(p);
     else if (wide)

@@ -31,7 +31,6 @@ __host__ __device__ inline size_t ds_block_offset(int bh, int nqt, int qt, int k
 // - LSE log2(e)) from Q, K and the saved LSE instead.  The dS blocks keep
 // their place in the state either way.
 constexpr int kShortHeadTiles = 2;
-constexpr int kBwdMaxSlots = 64;  // grid rows of the split dk/dv launch (key blocks + split parts)
 
 // Floats of the packed P' / dS blocks for a (B, H, T) problem.
 size_t bwd_ds_floats(int B, int H, int T);
@@ -86,20 +85,21 @@ struct BwdParams {
     const float *qb, *kb, *vb;
     float *dbq_part, *dbkv_part, *db;
     int C;
-    // Key blocks kb < nsplit (D = 64 kernels) are split by query range into
-    // two workgroups, which add their dK, dV parts into rows that the delta
-    // kernel zeroed (two addends: the sum is the same in either order).
-    // slot[s] = 2 kb + part is the work of grid row s (s = blockIdx / bh_pad),
-    // longest first; with nsplit == 0 the rows are the key blocks in order.
-    // The db partials then hold B * (nkb + nsplit) rows (part 1 of key
-    // block kb in row nkb + kb).
+    // Work lists of the D = 64 dk/dv kernel with the stored P' (block_sched.hpp):
+    // key blocks kb < nsplit are cut by query range into two items, which add
+    // their dK, dV parts into rows that the delta kernel zeroed (two addends:
+    // the sum is the same in either order).  The db partials then hold
+    // B * (nkb + nsplit) rows (the item that does not start on the diagonal
+    // writes row nkb + kb).
     int nsplit;
-    unsigned short slot[kBwdMaxSlots];
+    KeySched ksched;
+    int k_wg;  // workgroups of the work-list launch
 };
 
-// Sets p.nsplit and p.slot for the D = 64 dk/dv kernel of p's shape on the
-// current device (nsplit = 0 for the other kernels) and returns nsplit.
-int bwd_split_plan(BwdParams &p);
+// Sets p.nsplit, p.ksched and p.k_wg for the D = 64 dk/dv kernel of p's
+// shape on the current device (building and uploading the work lists on
+// `stream` on first use; nsplit = 0 for the other kernels) and returns nsplit.
+int bwd_split_plan(BwdParams &p, hipStream_t stream);
 
 // One KV-cache decode step (attn_decode.hip).
 struct DecParams {

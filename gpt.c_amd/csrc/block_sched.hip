@@ -102,6 +102,108 @@ SchedTable lpt_schedule(int BH, int nqt, int per_cu, int cus) {
     return t;
 }
 
+// ---- dk/dv key-block lists ----
+
+constexpr double kKeyItemOverhead = 0.3;  // V rows and epilogue of an item, in tiles
+// A workgroup left alone on its CU gets this share of what the CU's full set
+// of workgroups gets (measured: one wave per SIMD runs the C2 grid 253 us
+// against 206 us with two).
+constexpr double kAloneShare = 0.81;
+constexpr int kKeyTilesPerBlock = 2;        // 128 keys = 2 query tiles of 64 on the diagonal
+
+double key_cost(int kb, int qa, int qe) {
+    const int diag = kKeyTilesPerBlock * kb;
+    return (qe - qa) - (qa == diag ? 0.75 : 0.0) + kKeyItemOverhead;
+}
+
+KeyTable key_schedule_with(int BH, int nqt, int nsplit, int per_cu, int cus) {
+    struct Item {
+        double cost;
+        int bh, kb, qa, qe;
+    };
+    const int nkb = (nqt + kKeyTilesPerBlock - 1) / kKeyTilesPerBlock;
+    std::vector<Item> all;
+    for (int bh = 0; bh < BH; ++bh)
+        for (int kb = 0; kb < nkb; ++kb) {
+            const int qa = kKeyTilesPerBlock * kb, qe = nqt;
+            if (kb < nsplit && qe - qa >= 2) {
+                int best = qa + 1;
+                for (int m = qa + 1; m < qe; ++m)
+                    if (std::abs(key_cost(kb, qa, m) - key_cost(kb, m, qe)) <
+                        std::abs(key_cost(kb, qa, best) - key_cost(kb, best, qe)))
+                        best = m;
+                all.push_back({key_cost(kb, qa, best), bh, kb, qa, best});
+                all.push_back({key_cost(kb, best, qe), bh, kb, best, qe});
+            } else {
+                all.push_back({key_cost(kb, qa, qe), bh, kb, qa, qe});
+            }
+        }
+    // Heads dealt to XCDs in contiguous ranges of equal work (item granularity).
+    double total = 0.0;
+    for (const Item &it : all) total += it.cost;
+    const double target = total / kSchedXcds;
+    std::vector<std::vector<Item>> xitems(kSchedXcds);
+    double acc = 0.0;
+    for (const Item &it : all) {
+        const int x = std::min(static_cast<int>((acc + 0.5 * it.cost) / target), kSchedXcds - 1);
+        xitems[x].push_back(it);
+        acc += it.cost;
+    }
+    std::vector<std::vector<std::vector<std::vector<Item>>>> slots(
+        kSchedXcds, std::vector<std::vector<std::vector<Item>>>(cus, std::vector<std::vector<Item>>(per_cu)));
+    double est = 0.0;
+    int rounds = 1;
+    for (int x = 0; x < kSchedXcds; ++x) {
+        auto &its = xitems[x];
+        std::stable_sort(its.begin(), its.end(), [](const Item &a, const Item &b) { return a.cost > b.cost; });
+        std::vector<double> cu(cus, 0.0);
+        std::vector<std::vector<double>> sl(cus, std::vector<double>(per_cu, 0.0));
+        for (const Item &it : its) {
+            const int u = static_cast<int>(std::min_element(cu.begin(), cu.end()) - cu.begin());
+            const int s = static_cast<int>(std::min_element(sl[u].begin(), sl[u].end()) - sl[u].begin());
+            cu[u] += it.cost;
+            sl[u][s] += it.cost;
+            slots[x][u][s].push_back(it);
+        }
+        for (int u = 0; u < cus; ++u) {
+            // The heavier list on the slot dispatched first (older waves issue first).
+            std::vector<int> order(per_cu);
+            std::iota(order.begin(), order.end(), 0);
+            std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return sl[u][a] > sl[u][b]; });
+            std::vector<std::vector<Item>> sorted;
+            for (int s : order) sorted.push_back(std::move(slots[x][u][s]));
+            slots[x][u] = std::move(sorted);
+            int used = 0;
+            double longest = 0.0;
+            for (int s = 0; s < per_cu; ++s) {
+                if (!slots[x][u][s].empty()) used = s + 1;
+                longest = std::max(longest, sl[u][s]);
+            }
+            rounds = std::max(rounds, used);
+            // Time in tiles of one slot's share of the CU: the CU's total
+            // shared by its slots, or the longest list, which runs alone
+            // once the others are done.
+            const double alone = per_cu > 1 ? longest / (per_cu * kAloneShare) : longest;
+            est = std::max(est, std::max(cu[u] / per_cu, alone));
+        }
+    }
+    KeyTable t;
+    t.nsplit = nsplit;
+    t.est = est;
+    t.num_wg = kSchedXcds * cus * rounds;
+    t.wg_start.push_back(0);
+    int n = 0;
+    for (int w = 0; w < t.num_wg; ++w) {
+        const int x = w % kSchedXcds, i = w / kSchedXcds, u = i % cus, s = i / cus;
+        for (const Item &it : slots[x][u][s]) {
+            t.items.insert(t.items.end(), {it.bh, it.kb, it.qa, it.qe});
+            ++n;
+        }
+        t.wg_start.push_back(n);
+    }
+    return t;
+}
+
 struct DeviceTable {
     int num_wg = 0;
     int *wg_start = nullptr;
@@ -109,11 +211,47 @@ struct DeviceTable {
     SchedTable host;  // kept: the source of the stream-ordered upload
 };
 
+struct DeviceKeyTable {
+    int num_wg = 0, nsplit = 0;
+    int *wg_start = nullptr;
+    int *items = nullptr;
+    KeyTable host;  // kept: the source of the stream-ordered upload
+};
+
 std::mutex g_mu;
 std::map<std::tuple<int, int, int, int>, DeviceTable> g_tables;  // (device, BH, nqt, per_cu)
+std::map<std::tuple<int, int, int, int>, DeviceKeyTable> g_key_tables;  // (device, BH, nqt, per_cu)
 std::map<std::pair<int, const void *>, std::pair<int, int>> g_occupancy;  // (device, kernel) -> (per_cu, cus)
 
+// (workgroups per CU, CUs per XCD) of `kernel` on device dev; g_mu held.
+std::pair<int, int> occupancy_locked(int dev, const void *kernel) {
+    auto occ = g_occupancy.find({dev, kernel});
+    if (occ == g_occupancy.end()) {
+        int per_cu = 0, cus_total = 0;
+        hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0));
+        hipCheck(hipDeviceGetAttribute(&cus_total, hipDeviceAttributeMultiprocessorCount, dev));
+        const int cus = std::max(1, cus_total / kSchedXcds);
+        occ = g_occupancy.emplace(std::make_pair(dev, kernel), std::make_pair(std::max(1, per_cu), cus)).first;
+    }
+    return occ->second;
+}
+
 }  // namespace
+
+KeyTable build_key_schedule(int BH, int nqt, int per_cu, int cus) {
+    CHECK_ERROR(BH < 0 || nqt < 1 || per_cu < 1 || cus < 1, "key schedule: unsupported shape (heads %d, tiles %d, per CU %d, CUs %d).",
+                BH, nqt, per_cu, cus);
+    const int nkb = (nqt + kKeyTilesPerBlock - 1) / kKeyTilesPerBlock;
+    std::vector<KeyTable> cand;
+    double best = 0.0;
+    for (int ns = 0; ns <= nkb; ++ns) {
+        cand.push_back(key_schedule_with(BH, nqt, ns, per_cu, cus));
+        best = ns == 0 ? cand.back().est : std::min(best, cand.back().est);
+    }
+    for (KeyTable &t : cand)
+        if (t.est <= 1.02 * best) return std::move(t);
+    return std::move(cand.front());
+}
 
 SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus) {
     CHECK_ERROR(BH < 0 || nqt < 1 || nqt > (1 << kSchedJBits) || per_cu < 1 || cus < 1 ||
@@ -132,15 +270,8 @@ BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_
     int dev = 0;
     hipCheck(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_mu);
-    auto occ = g_occupancy.find({dev, kernel});
-    if (occ == g_occupancy.end()) {
-        int per_cu = 0, cus_total = 0;
-        hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0));
-        hipCheck(hipDeviceGetAttribute(&cus_total, hipDeviceAttributeMultiprocessorCount, dev));
-        const int cus = std::max(1, cus_total / kSchedXcds);
-        occ = g_occupancy.emplace(std::make_pair(dev, kernel), std::make_pair(std::max(1, per_cu), cus)).first;
-    }
-    const int per_cu = occ->second.first, cus = occ->second.second;
+    const auto occ = occupancy_locked(dev, kernel);
+    const int per_cu = occ.first, cus = occ.second;
     const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus);
     auto it = g_tables.find(key);
     if (it == g_tables.end()) {
@@ -160,6 +291,33 @@ BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_
     return BlockSched{it->second.wg_start, it->second.items};
 }
 
+KeySched device_key_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int *nsplit) {
+    int dev = 0;
+    hipCheck(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_mu);
+    const auto occ = occupancy_locked(dev, kernel);
+    const int per_cu = occ.first, cus = occ.second;
+    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus);
+    auto it = g_key_tables.find(key);
+    if (it == g_key_tables.end()) {
+        DeviceKeyTable d;
+        d.host = build_key_schedule(BH, nqt, per_cu, cus);
+        d.num_wg = d.host.num_wg;
+        d.nsplit = d.host.nsplit;
+        const size_t nw = d.host.wg_start.size() * sizeof(int), ni = std::max<size_t>(1, d.host.items.size()) * sizeof(int);
+        hipCheck(hipMalloc(&d.wg_start, nw));
+        hipCheck(hipMalloc(&d.items, ni));
+        hipCheck(hipMemcpyAsync(d.wg_start, d.host.wg_start.data(), nw, hipMemcpyHostToDevice, stream));
+        if (!d.host.items.empty())
+            hipCheck(hipMemcpyAsync(d.items, d.host.items.data(), d.host.items.size() * sizeof(int),
+                                    hipMemcpyHostToDevice, stream));
+        it = g_key_tables.emplace(key, std::move(d)).first;
+    }
+    *num_wg = it->second.num_wg;
+    *nsplit = it->second.nsplit;
+    return KeySched{it->second.wg_start, it->second.items};
+}
+
 }  // namespace gptc
 
 // Host-side view of a table, for tests: fills wg_start (num_wg + 1 ints)
@@ -173,5 +331,19 @@ extern "C" int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cu
     std::copy(t.items.begin(), t.items.end(), items);
     if (max_cu_load) *max_cu_load = t.max_cu_load;
     if (used_pairs) *used_pairs = t.pairs ? 1 : 0;
+    return t.num_wg;
+}
+
+// Host-side view of a dk/dv key-block table, for tests: fills wg_start
+// (num_wg + 1 ints, in items) and items (4 ints each, cap ints in all) and
+// returns num_wg (-1 if cap is too small).
+extern "C" int gptc_attention_key_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
+                                           double *est, int *nsplit) {
+    const gptc::KeyTable t = gptc::build_key_schedule(BH, nqt, per_cu, cus);
+    if (static_cast<int>(t.items.size()) > cap || t.num_wg + 1 > cap) return -1;
+    std::copy(t.wg_start.begin(), t.wg_start.end(), wg_start);
+    std::copy(t.items.begin(), t.items.end(), items);
+    if (est) *est = t.est;
+    if (nsplit) *nsplit = t.nsplit;
     return t.num_wg;
 }

@@ -59,4 +59,43 @@ SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus);
 // first use and cached for the life of the process.
 BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg);
 
+// ---- Work lists of the D = 64 dk/dv kernel ----
+//
+// The unit of work is one 128-key block kb of one head: query tiles
+// 2kb .. nqt-1 (the first two hold the diagonal).  Key block kb of head bh
+// costs nqt - 2kb tiles, less 3/4 for the diagonal's two partly masked tiles,
+// plus a fixed part (V rows, epilogue).  The blocks of a head therefore range
+// from about 1 to nqt tiles, and a grid of one workgroup per block leaves the
+// CUs that hold the longest blocks busy long after the others.  Here each
+// workgroup runs a list of items, one after the other:
+//   items[4i .. 4i+3] = (bh, kb, qa, qe): query tiles [qa, qe) of key block
+//   kb of head bh.
+// Key blocks kb < nsplit (the same for every head) are cut in two at a tile
+// edge into items of about equal cost, whose dK, dV the kernel adds into rows
+// the delta kernel zeroed (two addends: the same sum in either order).
+// Every other block is one item.  The items are placed like the query-block
+// lists (heads dealt to the XCDs in contiguous ranges of equal work, longest
+// first onto the least-loaded CU, then its least-loaded slot), and the CU's
+// heavier list goes to the slot dispatched first.  nsplit is the smallest
+// count whose estimated time (a CU's total, or its longest list run alone)
+// is within 2 % of the best over 0 .. nkb.
+struct KeySched {
+    const int *wg_start;  // num_wg + 1 offsets into items (in items, not ints)
+    const int *items;     // 4 ints per item
+};
+
+struct KeyTable {
+    int num_wg = 0;
+    int nsplit = 0;
+    std::vector<int> wg_start, items;
+    double est = 0.0;  // the estimated time the choice of nsplit minimised (tiles)
+};
+
+KeyTable build_key_schedule(int BH, int nqt, int per_cu, int cus);
+
+// The device copy of build_key_schedule for the current device and the
+// residency of `kernel`, built, uploaded (stream-ordered on `stream`) and
+// cached like device_block_schedule.
+KeySched device_key_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int *nsplit);
+
 }  // namespace gptc

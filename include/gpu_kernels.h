@@ -78,7 +78,9 @@ void copy_tensor_data_cuda(tensor_t *dst, const tensor_t *src);
  *   gives the same result.  The backward consumes cache[3] (its dS
  *   overwrites the stored probabilities), as gpt.c's backward, which
  *   frees the cache right after (attention.c:147-155), permits; a second
- *   backward needs a new forward.  It allocates nothing.
+ *   backward needs a new forward.  It allocates nothing per call: the work
+ *   lists of its D = 64 kernels (a few KB per shape) are built and uploaded
+ *   on the first backward of a shape and kept for the life of the process.
  */
 void attention_forward_cuda_kernel(
     const tensor_t *input,
@@ -278,6 +280,18 @@ long long gptc_decode_noalloc_scratch_floats(void);
  *   Returns the workgroup count (-1 when cap ints do not hold the table);
  *   max_cu_load receives the largest per-CU sum of block costs (j + 1.5
  *   tiles each), used_pairs 1 when the pairs construction was chosen.
+ *
+ * gptc_attention_key_schedule(BH, nqt, per_cu, cus, wg_start, items, cap,
+ *                             est, nsplit)
+ *   The work lists the D = 64 dk/dv kernel runs for BH heads of nqt 64-query
+ *   tiles (128-key blocks kb = 0 .. ceil(nqt / 2) - 1, block kb reducing
+ *   tiles 2kb .. nqt-1), on the same GPU description (host computation only,
+ *   for tests and tuning): workgroup w runs items wg_start[w] ..
+ *   wg_start[w+1]), item i being items[4i .. 4i+3] = (bh, kb, qa, qe), query
+ *   tiles [qa, qe) of key block kb of head bh.  Blocks kb < *nsplit are cut
+ *   into two items, the others are one.  Returns the workgroup count (-1 when
+ *   cap ints do not hold the table); est receives the estimated time (tiles)
+ *   the choice of nsplit minimised.
  */
 /*
  * ---- one-token model step (KV-cache generation): no counterpart in gpt.c ----
@@ -313,6 +327,8 @@ long long gptc_attention_state_floats(int B, int T, int C, int n_heads);
 long long gptc_attention_set_state_limit(long long floats);
 int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
                                   double *max_cu_load, int *used_pairs);
+int gptc_attention_key_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
+                                double *est, int *nsplit);
 
 #ifdef __cplusplus
 }

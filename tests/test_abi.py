@@ -179,3 +179,55 @@ def test_block_schedule_balances_c5(lib):
     share = BH * sum(j + 1.5 for j in range(nqt)) / (8 * 32)
     assert not pairs and n <= 8 * 32 * 3
     assert load <= 1.05 * share, (load, share)
+
+
+def key_schedule(lib, BH, nqt, per_cu=2, cus=32):
+    nkb = (nqt + 1) // 2
+    cap = 4 * (2 * BH * nkb) + 8 * cus * per_cu * 2 + 16
+    ws, it = (ctypes.c_int * cap)(), (ctypes.c_int * cap)()
+    est, nsplit = ctypes.c_double(), ctypes.c_int()
+    n = lib.gptc_attention_key_schedule(BH, nqt, per_cu, cus, ws, it, cap, ctypes.byref(est), ctypes.byref(nsplit))
+    assert n > 0
+    starts = list(ws[:n + 1])
+    items = [tuple(it[4 * i:4 * i + 4]) for i in range(starts[-1])]
+    return n, starts, items, est.value, nsplit.value
+
+
+@pytest.mark.parametrize("B,H,T", [(8, 12, 1024), (4, 25, 1024), (8, 12, 256), (1, 12, 1024), (8, 12, 960),
+                                   (3, 7, 2000), (16, 25, 1024), (32, 12, 1024), (1, 1, 200), (2, 12, 4096)])
+def test_key_schedule_covers_every_tile_once(lib, B, H, T):
+    """The dk/dv kernel writes dK, dV rows of exactly the items its work lists
+    name: the items of every (head, 128-key block kb) must cover query tiles
+    2kb .. nqt-1 once, as one item, or as two for kb < nsplit (whose adds land
+    on rows the delta kernel zeroed: two addends give the same sum in either
+    order, three would not)."""
+    BH, nqt = B * H, (T + 63) // 64
+    nkb = (nqt + 1) // 2
+    n, starts, items, est, nsplit = key_schedule(lib, BH, nqt)
+    assert n % 8 == 0 and starts[0] == 0 and all(a <= b for a, b in zip(starts, starts[1:]))
+    assert 0 <= nsplit <= nkb
+    by_block = {}
+    for bh, kb, qa, qe in items:
+        assert 0 <= bh < BH and 0 <= kb < nkb and 2 * kb <= qa < qe <= nqt
+        by_block.setdefault((bh, kb), []).append((qa, qe))
+    assert sorted(by_block) == [(bh, kb) for bh in range(BH) for kb in range(nkb)]
+    for (bh, kb), parts in by_block.items():
+        parts.sort()
+        assert parts[0][0] == 2 * kb and parts[-1][1] == nqt
+        assert all(a[1] == b[0] for a, b in zip(parts, parts[1:]))
+        assert len(parts) <= (2 if kb < nsplit else 1), ((bh, kb), parts, nsplit)
+
+
+def test_key_schedule_c2_balance(lib):
+    """At C2 (96 heads x 8 key blocks over 512 slots) the lists need no split
+    and keep every CU within 5 % of the even share of the work."""
+    BH, nqt = 96, 16
+    n, starts, items, est, nsplit = key_schedule(lib, BH, nqt)
+    cost = lambda kb, qa, qe: (qe - qa) - (0.75 if qa == 2 * kb else 0.0) + 0.3
+    share = BH * sum(cost(kb, 2 * kb, nqt) for kb in range(nqt // 2)) / (8 * 32)
+    assert nsplit == 0 and n == 512
+    loads = {}
+    for w in range(n):
+        cu = (w % 8, (w // 8) % 32)
+        loads[cu] = loads.get(cu, 0.0) + sum(cost(kb, qa, qe) for (bh, kb, qa, qe) in items[starts[w]:starts[w + 1]])
+    assert max(loads.values()) <= 1.05 * share, (max(loads.values()), share)
