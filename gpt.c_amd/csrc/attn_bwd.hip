@@ -881,7 +881,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
             return true;
         }
         if (++sit >= it_end) return false;
-        const int item = a.sched.items[sit];
+        const int item = load_uniform_int(a.sched.items + sit);
         sbh = sched_bh(item);
         sj = sched_j(item);
         skt = 0;
@@ -1054,7 +1054,7 @@ attn_bwd_dq16_recomp_kernel(const BwdParams a) {
             return true;
         }
         if (++sit >= it_end) return false;
-        const int item = a.sched.items[sit];
+        const int item = load_uniform_int(a.sched.items + sit);
         sbh = sched_bh(item);
         sj = sched_j(item);
         skt = 0;

@@ -94,6 +94,17 @@ using IntC = std::integral_constant<int, N>;
 
 __device__ __forceinline__ uint32_t uniform(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// An int at a uniform address of memory that no kernel writes (the work
+// lists), read through the scalar data cache.  The compiler reads such an
+// entry inside a loop with a vector load, and its wait for that load also
+// waits for every tile load in flight (a full memory round trip at each
+// block change); this waits for the scalar load alone.
+__device__ __forceinline__ int load_uniform_int(const int *p) {
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
+
 template <typename T>
 __device__ __forceinline__ T *uniform(T *p) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);

@@ -412,7 +412,7 @@ attn_fwd16_kernel(const FwdParams a) {
             return true;
         }
         if (++sit >= it_end) return false;
-        const int item = a.sched.items[sit];
+        const int item = load_uniform_int(a.sched.items + sit);
         sbh = sched_bh(item);
         sj = sched_j(item);
         skt = 0;
