@@ -1044,6 +1044,7 @@ attn_bwd_dq16_recomp_kernel(const BwdParams a) {
     const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
     const int it_end = a.sched.wg_start[blockIdx.x + 1];
     int it = a.sched.wg_start[blockIdx.x];
+    const int it_first = it;  // a register: re-reading the table would wait for every load in flight
     if (it >= it_end) return;
     const int T = a.T;
     const float c2 = a.scale * kLog2e;
@@ -1156,7 +1157,7 @@ attn_bwd_dq16_recomp_kernel(const BwdParams a) {
 
     for (;;) {
         if (kt == 0) {
-            if (it != a.sched.wg_start[blockIdx.x]) load_rows();
+            if (it != it_first) load_rows();
 #pragma unroll
             for (int db = 0; db < 4; ++db) acc[db] = zero4();
         }

@@ -373,6 +373,7 @@ attn_fwd16_kernel(const FwdParams a) {
     const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
     const int it_end = a.sched.wg_start[blockIdx.x + 1];
     int it = a.sched.wg_start[blockIdx.x];
+    const int it_first = it;  // a register: re-reading the table would wait for every load in flight
     if (it >= it_end) return;
     const int T = a.T, nqt = a.nqt;
 
@@ -474,7 +475,7 @@ attn_fwd16_kernel(const FwdParams a) {
         if (kt == 0) {
             // A new block: fresh statistics (its Q rows are loaded already
             // for the first block, here for the others).
-            if (it != a.sched.wg_start[blockIdx.x]) load_q();
+            if (it != it_first) load_q();
             if (PERM && my_q < T) {
                 float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * kDPad + 16 * g;
 #pragma unroll
