@@ -741,13 +741,16 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     // The qkv bias: key rows past T then hold the bias; they are masked for
     // every query < T, and rows of queries past T are not written.
     const bool biased = a.kb != nullptr;
-    f32x4 qr[4];
+    // The Q rows and bias are requested here and added in piece(), after
+    // the K and V requests, so that no wait comes before those are issued.
+    f32x4 qr[4], qb4[4];
     if (sj >= 0) {
         const int q = sj * kF16Rows + 16 * ss + i16;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * c + 4 * g);
-            if (biased) qr[c] += *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * c + 4 * g);
+        for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * c + 4 * g);
+        if (biased) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) qb4[c] = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * c + 4 * g);
         }
     }
 
@@ -780,6 +783,7 @@ attn_fwd_twotile_kernel(const FwdParams a) {
             const f32x4 vb4 = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 4 * i16);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
+                qr[c] += qb4[c];
                 const f32x4 kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + 16 * c + 4 * g);
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
