@@ -718,6 +718,9 @@ struct SlabState {
 
 constexpr int kTwoTileRoles = 4;  // workgroups per head
 
+// BIAS: the qkv bias is added to the loaded rows (a.qb, a.kb, a.vb set); a
+// separate build, so that the other keeps no registers for it.
+template <bool BIAS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 attn_fwd_twotile_kernel(const FwdParams a) {
     __shared__ __attribute__((aligned(16))) f32x4 part_lds[2][5][64];  // [partial][acc0..3, {m, l}][lane]
@@ -740,7 +743,7 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     const int sj = kJobSlab[job][0], ss = kJobSlab[job][1];
     // The qkv bias: key rows past T then hold the bias; they are masked for
     // every query < T, and rows of queries past T are not written.
-    const bool biased = a.kb != nullptr;
+    constexpr bool biased = BIAS;
     // The Q rows and bias are requested here and added in piece(), after
     // the K and V requests, so that no wait comes before those are issued.
     f32x4 qr[4], qb4[4];
@@ -874,7 +877,10 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
         if (deep && !perm) {
             if (ev) hipCheck(hipEventRecord(ev[0], stream));
             if (p.nqt == 2)
-                attn_fwd_twotile_kernel<<<dim3(kTwoTileRoles * p.B * p.H), dim3(256), 0, stream>>>(p);
+                if (p.kb != nullptr)
+                    attn_fwd_twotile_kernel<true><<<dim3(kTwoTileRoles * p.B * p.H), dim3(256), 0, stream>>>(p);
+                else
+                    attn_fwd_twotile_kernel<false><<<dim3(kTwoTileRoles * p.B * p.H), dim3(256), 0, stream>>>(p);
             else
                 attn_fwd_short_kernel<<<dim3(p.B * p.H * p.nqt), dim3(256), 0, stream>>>(p);
             hipCheck(hipGetLastError());
