@@ -572,9 +572,9 @@ extern "C" long long gptc_decode_noalloc_scratch_floats(void) {
     return static_cast<long long>(kDecodeScratchFloats);
 }
 
-void gptc::attention_decode_devpos(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int *pos_dev,
-                                   const int n_heads, tensor_t *output, float *part) {
-    decode_step(qkv, k_cache, v_cache, 0, pos_dev, n_heads, output, part);
+void gptc::attention_decode_cached(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, const int pos,
+                                   const int *pos_dev, const int n_heads, tensor_t *output, float *part) {
+    decode_step(qkv, k_cache, v_cache, pos, pos_dev, n_heads, output, part);
 }
 
 size_t gptc::attention_decode_part_floats(const int B, const int H, const int L) {

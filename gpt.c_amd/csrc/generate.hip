@@ -38,10 +38,7 @@ void step_body(gpt2_t *gpt, gptc_kv_cache_t *kv, int pos, const int *pos_dev, te
         const self_attention_t *sa = blk->attn;
         const mlp_t *mlp = blk->mlp;
         ln_linear_rows(blk->ln1->W, blk->ln1->b, blk->ln1->eps, sa->qkv->W, sa->qkv->b, s[S_X], NULL, 0, s[S_QKV]);
-        if (pos_dev != nullptr)
-            attention_decode_devpos(s[S_QKV], kv->k[l], kv->v[l], pos_dev, gpt->n_heads, s[S_A], s[S_PART]->t);
-        else
-            attention_decode_cuda_kernel(s[S_QKV], kv->k[l], kv->v[l], pos, gpt->n_heads, s[S_A]);
+        attention_decode_cached(s[S_QKV], kv->k[l], kv->v[l], pos, pos_dev, gpt->n_heads, s[S_A], s[S_PART]->t);
         gptc_linear_rows_cuda(sa->c_proj->W, sa->c_proj->b, s[S_A], s[S_X], 0, s[S_X2]);
         ln_linear_rows(blk->ln2->W, blk->ln2->b, blk->ln2->eps, mlp->c_fc->W, mlp->c_fc->b, s[S_X2], NULL, 1,
                        s[S_F]);
