@@ -428,14 +428,10 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 // load instruction gathers 16 dims of 4 consecutive rows (4 pieces of 64
 // bytes) into 64 consecutive LDS words.
 //
-// The compiler does not see these loads: the wait for them is an explicit
-// s_waitcnt vmcnt(0) (through the builtin, so that the compiler's own
-// counting knows every earlier load has landed) right before that barrier.
-// Loads the compiler issues later are younger than the tile's, so its own
-// waits can only over-wait, never under-wait.  The asm sets M0 (the LDS
-// address of the row) before each load; the compiler ignores an M0 clobber,
-// and its code for this kernel uses M0 nowhere else (gfx950's DS
-// instructions do not read it; checked in the generated code).
+// The loads are __builtin_amdgcn_raw_ptr_buffer_load_lds: the compiler sets
+// M0 (the LDS address of the instruction's 64 words) and counts them.  The
+// wait for a tile is an explicit s_waitcnt vmcnt(0) right before the barrier
+// that publishes it; every LDS read of that buffer comes after the barrier.
 //
 // At the end of an item its dK, dV rows are stored (added, for the two items
 // of a key block kb < nsplit), then the next item's V rows are loaded.
@@ -512,8 +508,8 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         }
     };
 
-    // Rows 16w .. 16w+15 of the step's tile into LDS buffer buf (M0 = the LDS
-    // byte address the instruction's 64 words start at).  dO: row q0 + i,
+    // Rows 16w .. 16w+15 of the step's tile into LDS buffer buf (mq, md: the
+    // LDS byte address an instruction's 64 words start at).  dO: row q0 + i,
     // lane -> dim.  Q: instruction i takes rows q0 + 4(i/4) + (lane % 4), dims
     // 16(i % 4) + lane / 4, i.e. group q4 = 4w + i/4 of the tile, words
     // [64(i % 4), 64(i % 4) + 64) of the group's 256.
@@ -534,13 +530,10 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         for (int i = 0; i < 16; ++i) {
             const uint32_t q = q0 + i;
             const uint32_t gq = q0 + 4 * (i >> 2);
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(
-                             mq + (i >> 2) * (4u * kDPad * 4u) + (i & 3) * 256u),
-                         "v"(gq * a.q.st * 4u + (i & 3) * 64u + vq), "s"(q_rows)
-                         : "memory");
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(md + i * LS * 4u),
-                         "v"(q * a.dout.st * 4u + vl), "s"(do_rows)
-                         : "memory");
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rows, lds_ptr(mq + (i >> 2) * (4u * kDPad * 4u) + (i & 3) * 256u),
+                                                     4, gq * a.q.st * 4u + (i & 3) * 64u + vq, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(do_rows, lds_ptr(md + i * LS * 4u), 4,
+                                                     q * a.dout.st * 4u + vl, 0, 0, 0);
         }
     };
     // The statistics of a step, loaded one step ahead (see attn_bwd_dkdv_kernel).

@@ -120,6 +120,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rows(const float *base, i
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(uniform(base)), 0, bytes, kBufferConfig);
 }
 
+// The LDS pointer at a wave-uniform LDS byte address: the destination of a
+// buffer load that writes LDS directly (__builtin_amdgcn_raw_ptr_buffer_load_lds;
+// the compiler sets M0 from it and counts the load in its own waits).
+__device__ __forceinline__ __attribute__((address_space(3))) void *lds_ptr(uint32_t byte_addr) {
+    return reinterpret_cast<__attribute__((address_space(3))) void *>(static_cast<uintptr_t>(uniform(byte_addr)));
+}
+
 // Four floats at float offset `off` of a buffer resource.
 __device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0));
