@@ -41,6 +41,7 @@ SEED_X, SEED_DY = 1337, 1338
 SPEC_CU, SPEC_MHZ = 256, 2400            # MI355X public spec
 FLOP_PER_CLK_CU_FP32_MFMA = 256          # v_mfma_f32_32x32x2_f32: 4096 flop / 16 passes of 4 clk, 4 SIMDs
 HBM_PEAK_GBS = 8000.0
+BOX_CPU_SHARE = 16                       # CPUs a one-GPU box allots to a job
 
 
 def log(*a):
@@ -98,21 +99,57 @@ class Hip:
         self.check(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
 
 
+def host_cpu():
+    """The host CPU as the CPU baselines use it: lscpu's model, threads per
+    core, cores per socket and sockets, the logical CPUs this process may run
+    on (its affinity set) and the physical cores behind them (distinct
+    (package, core) pairs in sysfs).  OpenBLAS runs one thread per physical
+    core of that set, capped at BOX_CPU_SHARE, the CPUs a one-GPU box
+    allots to a job whatever the machine has."""
+    info = {"nproc": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=30).stdout
+        for key, name in (("Model name", "model"), ("Thread(s) per core", "threads_per_core"),
+                          ("Core(s) per socket", "cores_per_socket"), ("Socket(s)", "sockets")):
+            m = re.search(rf"^{re.escape(key)}:\s*(.+)$", out, re.M)
+            if m:
+                v = m.group(1).strip()
+                info[name] = int(v) if v.isdigit() else v
+    except (OSError, subprocess.SubprocessError):
+        pass
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id") as f:
+                core = f.read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    info["affinity_logical_cpus"] = len(cpus)
+    info["affinity_physical_cores"] = len(cores)
+    info["openblas_threads"] = max(1, min(len(cores), BOX_CPU_SHARE))
+    return info
+
+
 def contraction_flops(B, T, H, D):
     return float(D) * T * (T + 1) * B * H
 
 
-def cpu_baseline(cfg, x, dy, budget_s, gpu_out=None):
+def cpu_baseline(cfg, x, dy, budget_s, gpu_outs=None):
     """The oracle (C restatement of gpt.c's OpenBLAS CPU path) on this host,
     forward + backward (forward only for a forward-only config).
 
-    gpu_out = {"y", "lse", "dqkv"} of the timed GPU steps on the same inputs:
-    the last oracle run checks them (max abs error per output; the LSE
-    against a float64 log-sum-exp of the oracle's q, k), as the parity tests
-    do."""
+    gpu_outs = {name: {"y", "lse", "dqkv"}} of timed GPU steps on the same
+    inputs: the last oracle run checks each (max abs error per output; the
+    LSE against a float64 log-sum-exp of the oracle's q, k), as the parity
+    tests do.  The errors come back per name."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as oracle_mod
-    threads = min(16, os.cpu_count() or 1)
+    cpu = host_cpu()
+    threads = cpu["openblas_threads"]
     orc = oracle_mod.Oracle(threads=threads)
     B, T, C, H = cfg["B"], cfg["T"], cfg["C"], cfg["H"]
     fwd_only = bool(cfg.get("forward_only"))
@@ -131,33 +168,29 @@ def cpu_baseline(cfg, x, dy, budget_s, gpu_out=None):
             break
     fwd = statistics.median(t[0] for t in times)
     bwd = statistics.median(t[1] for t in times)
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            m = re.search(r"model name\s*:\s*(.*)", f.read())
-            model = m.group(1).strip() if m else ""
-    except OSError:
-        pass
-    err = None
-    if gpu_out is not None:
+    errs = {}
+    lse_ref = lse_fp64(q, k) if gpu_outs else None
+    for name, gpu_out in (gpu_outs or {}).items():
         def e(a, b):
             return float(np.abs(a.astype(np.float64) - b).max())
-        err = {"y": e(gpu_out["y"], y_ref), "lse": e(gpu_out["lse"], lse_fp64(q, k))}
+        err = {"y": e(gpu_out["y"], y_ref), "lse": e(gpu_out["lse"], lse_ref)}
         if not fwd_only:
             d = gpu_out["dqkv"]
             err.update(dq=e(d[..., :C], d_ref[..., :C]), dk=e(d[..., C:2 * C], d_ref[..., C:2 * C]),
                        dv=e(d[..., 2 * C:], d_ref[..., 2 * C:]))
         err["tolerance"] = 1e-4
+        errs[name] = err
     sample = (f"one full {cfg['workload']} call (B={B} T={T} H={H}), 1 warm-up then median of {len(times)}; "
               f"fwd {fwd * 1e3:.1f} ms" + ("" if fwd_only else f" + bwd {bwd * 1e3:.1f} ms") +
-              f"; OPENBLAS threads={threads}; {orc.blas_config}; host '{model}', nproc={os.cpu_count()}")
+              f"; OPENBLAS threads={threads} (one per physical core of the affinity set, at most "
+              f"{BOX_CPU_SHARE}); {orc.blas_config}")
     if fwd_only:
         fwd_bytes, _ = compulsory_bytes(B, T, C, H)
         value, unit, ms = fwd_bytes / fwd / 1e9, "GB/s", fwd * 1e3
     else:
         value, unit, ms = 6 * contraction_flops(B, T, H, C // H) / (fwd + bwd) / 1e12, "TFLOP/s", (fwd + bwd) * 1e3
     return {"value": value, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
-            "ms_per_step": ms, "gpu_max_abs_err": err}
+            "ms_per_step": ms, "host": cpu, "openblas": orc.blas_config, "gpu_max_abs_err": errs}
 
 
 def copy_calibration(args):
@@ -192,16 +225,26 @@ def copy_calibration(args):
 
 
 def decode_bench(args):
-    """C4: KV-cache decode at GPT-2 small's heads (B=1, C=768, H=12), one layer.
+    """C4's attention: the KV-cache decode step at GPT-2 small's heads (B=1,
+    C=768, H=12), over the caches of --decode-layers layers (default 12, the
+    model's depth, so that the K/V set per position is the model's, not one
+    layer's that would stay in L2).
 
     A 64-token prompt fills the caches, then 448 generated tokens (positions
-    64..511) are timed, one attention_decode_cuda_kernel call each, inputs
-    resident in HBM.  Beside it: the reference-literal step, gpt.c's
-    infer_gpt.c:339-351 recompute of the full 1024-token window through
-    attention_forward_cuda_kernel for every token.
+    64..511) are timed, one attention_decode_cuda_kernel call per layer each,
+    inputs resident in HBM: exactly K = 448 x layers back-to-back launches
+    between two events on the library stream.  Metric: compulsory HBM bytes per step (cached K
+    and V rows 0..pos-1 read once, the new q, k, v row read, its k, v and the
+    output row written) over the time per step.  Every step is one kernel
+    (attn_decode_head_kernel), so the roofline's duration is the same
+    interval: the launch-to-launch time, kernel plus dispatch gap.
+    Beside it: the reference-literal step, gpt.c's infer_gpt.c:339-351
+    recompute of the full 1024-token window, through this library's forward
+    and (cpu_baseline) through the oracle on the host.
     """
     B, C, H, L, prompt, last = 1, 768, 12, 1024, 64, 512
     D = C // H
+    layers = args.decode_layers
     lib = gptc.load()
     rt = gptc.Runtime(lib)
     rt.init()
@@ -209,22 +252,28 @@ def decode_bench(args):
     stream = rt.stream()
     x = rt.normal((B, last, 3 * C), SEED_X)
     rows = [rt.from_numpy(x[:, p:p + 1, :]) for p in range(last)]
-    kc, vc, out = rt.empty((B, H, L, D)), rt.empty((B, H, L, D)), rt.empty((B, 1, C))
+    kvs = [(rt.empty((B, H, L, D)), rt.empty((B, H, L, D))) for _ in range(layers)]
+    out = rt.empty((B, 1, C))
     for p in range(prompt):
-        lib.attention_decode_cuda_kernel(rows[p], kc, vc, p, H, out)
+        for kc, vc in kvs:
+            lib.attention_decode_cuda_kernel(rows[p], kc, vc, p, H, out)
     rt.sync()
     hip.device_sync()
     a, b = hip.event(), hip.event()
     hip.record(a, stream)
     for p in range(prompt, last):
-        lib.attention_decode_cuda_kernel(rows[p], kc, vc, p, H, out)
+        for kc, vc in kvs:
+            lib.attention_decode_cuda_kernel(rows[p], kc, vc, p, H, out)
     hip.record(b, stream)
     steps = last - prompt
-    us = hip.elapsed_ms(a, b) * 1e3 / steps
-    # Compulsory bytes: every cached key and value row read once, the new row read, k, v and y written.
-    kv_bytes = sum(2 * (p + 1) * C * 4 for p in range(prompt, last))
+    us = hip.elapsed_ms(a, b) * 1e3 / (steps * layers)
+    y_last = rt.to_numpy(out)
+    # Compulsory bytes: cached key and value rows 0..pos-1 read once, the new
+    # q, k, v row read, its k, v written to the caches and the output row.
+    kv_bytes = sum(2 * p * C * 4 for p in range(prompt, last))
     io_bytes = steps * (3 * C + 2 * C + C) * 4
-    gbs = (kv_bytes + io_bytes) / (us * 1e-6 * steps) / 1e9
+    step_bytes = (kv_bytes + io_bytes) / steps
+    gbs = step_bytes / (us * 1e-6) / 1e9
 
     # Reference-literal: forward over the full window for every token.
     xw = rt.from_numpy(rt.normal((B, L, 3 * C), SEED_X))
@@ -240,17 +289,77 @@ def decode_bench(args):
         lib.attention_forward_cuda_kernel(xw, mask, H, caches, yw)
     hip.record(b, stream)
     win_us = hip.elapsed_ms(a, b) * 1e3 / args.steps
-    print(json.dumps({
-        "workload": "C4 KV-cache decode, B=1 C=768 H=12 (GPT-2 small heads), positions 64..511, one layer",
-        "us_per_step": round(us, 3), "GB_per_s": round(gbs, 1), "hbm_peak_GB_per_s": HBM_PEAK_GBS,
-        "bytes_per_step": round((kv_bytes + io_bytes) / steps),
+
+    kernel = "attn_decode_head_kernel"
+    roof = {"kernel": kernel, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": None, "algorithmic_bytes_per_launch": round(step_bytes),
+            "duration_ms": round(us * 1e-3, 6),
+            "duration_source": "the timed region: K back-to-back decode launches (one kernel each) between two "
+                               "events, / K (kernel plus dispatch gap)"}
+    traffic_file = os.path.join(ROOT, "profiles", "hbm_traffic_decode.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as fh:
+            tr = json.load(fh)
+        k = tr["kernels"].get(kernel)
+        if k:
+            roof["traffic"] = k["read_bytes"] + k["write_bytes"]
+            roof["traffic_source"] = (f"profiles/hbm_traffic_decode.json (rocprofv3 FETCH_SIZE x{tr['fetch_scale']:.2f}"
+                                      f" + WRITE_SIZE x{tr['write_scale']:.2f}, mean over the K launches)")
+    result = {
+        "metric": "C4 decode attention step, compulsory HBM GB/s, B=1 C=768 H=12 D=64, positions 64..511",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": prompt,
+        "ms_per_step": round(us * 1e-3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "step": "one decode launch: one layer's attention for one position",
+        "dtype": "fp32", "data": f"synthetic: qkv rows ~ N(0,1) seed {SEED_X} (torch-identical mt19937)",
+        "config": {"workload": f"C4 KV-cache decode attention, GPT-2 small's heads (B=1, C=768, H=12) over {layers} "
+                               "layers' caches, a 64-token prompt then positions 64..511", "B": B, "C": C, "H": H,
+                   "D": D, "L": L, "layers": layers},
+        "us_per_step": round(us, 3), "bytes_per_step": round(step_bytes),
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 3),
         "window_forward_us_per_step": round(win_us, 2),
         "speedup_vs_window_recompute": round(win_us / us, 1),
-        "note": "latency bound at B=1: 4 L D flop and 8 L D bytes per head per step",
-    }), flush=True)
-    for t in rows + [kc, vc, out, xw, mask, yw, *caches[1:]]:
+        "roofline": roof,
+        "note": "latency bound at B=1: 12 workgroups (one per head), one memory round trip per launch",
+    }
+    for t in rows + [t for kv in kvs for t in kv] + [out, xw, mask, yw, *caches[1:]]:
         rt.free(t)
     rt.sync()
+
+    if args.no_cpu_baseline:
+        result["cpu_baseline"] = None
+    else:
+        # gpt.c's own per-token attention work at C4 (infer_gpt.c:339-351): the
+        # oracle's forward over the whole block_size window, on the host; the
+        # value is the rate at which it yields the same output rows, in the
+        # GPU metric's unit (the decode step's compulsory bytes per token).
+        # Its window row 511 also checks the last timed decode output.
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as oracle_mod
+        cpu = host_cpu()
+        orc = oracle_mod.Oracle(threads=cpu["openblas_threads"])
+        xwin = np.concatenate([x, rt.normal((B, L, 3 * C), SEED_X + 7)[:, last:]], axis=1)
+        times = []
+        t_start = time.perf_counter()
+        y_ref = None
+        for i in range(6):
+            t0 = time.perf_counter()
+            y_ref, *_ = orc.forward(xwin, H)
+            times.append(time.perf_counter() - t0)
+            if i >= 2 and time.perf_counter() - t_start > args.cpu_budget_s:
+                break
+        sec = statistics.median(times[1:])
+        err = float(np.abs(y_last[:, 0].astype(np.float64) - y_ref[:, last - 1]).max())
+        result["cpu_baseline"] = {
+            "value": round(step_bytes / sec / 1e9, 4), "unit": "GB/s", "cores": cpu["openblas_threads"],
+            "kind": "port", "ms_per_step": round(sec * 1e3, 3),
+            "sample": (f"gpt.c's per-token step at C4: the oracle's forward over the full {L}-token window "
+                       f"(B=1, H={H}), warm-up then median of {len(times) - 1}: {sec * 1e3:.1f} ms per token; "
+                       f"OPENBLAS threads={cpu['openblas_threads']} (one per physical core of the affinity set, "
+                       f"at most {BOX_CPU_SHARE}); {orc.blas_config}"),
+            "host": cpu,
+            "gpu_max_abs_err": {"y_pos511_vs_window_row": err, "tolerance": 1e-4},
+        }
+    print(json.dumps(result), flush=True)
 
 
 def gpt2_step_flops(B, T, L, C, V):
@@ -345,7 +454,8 @@ def gpt2_cpu_baseline(rt, V, block, L, H, C):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as oracle_mod
     from gpt2_oracle import GPT2Oracle, param_shapes
-    threads = min(16, os.cpu_count() or 1)
+    cpu = host_cpu()
+    threads = cpu["openblas_threads"]
     orc = oracle_mod.Oracle(threads=threads)
     params = []
     for i, (name, shp) in enumerate(param_shapes(V, block, L, C)):
@@ -370,7 +480,9 @@ def gpt2_cpu_baseline(rt, V, block, L, H, C):
     sec = statistics.median(times[1:])
     return {"value": round(block / sec, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": (f"one GPT-2 124M training step at B=1 T={block} (1/8 of C3's batch), warm-up then median "
-                       f"of 2: {sec:.2f} s; OPENBLAS threads={threads}; {orc.blas_config}")}
+                       f"of 2: {sec:.2f} s; OPENBLAS threads={threads} (one per physical core of the affinity "
+                       f"set, at most {BOX_CPU_SHARE}); {orc.blas_config}"),
+            "host": cpu}
 
 
 def gpt2_bench(args):
@@ -638,6 +750,52 @@ def attention_bench(args):
         rt.sync()
         for t in srcs + dsts:
             rt.free(t)
+    # The LSE-only state (the north star's backward: P recomputed from the
+    # saved log-sum-exp; dS handed to the dq kernel through a scratch), timed
+    # the same way in the same process: the state limit at 0 makes every
+    # D = 64 forward keep only the LSE.  The first forward re-points cache[3]
+    # to the shorter state (outside the timed region).
+    lse_res, lse_out = None, None
+    if not fwd_only and D == 64:
+        prev_limit = lib.gptc_attention_set_state_limit(0)
+        for _ in range(args.warmup):
+            step()
+        rt.sync()
+        ms_lse = timed(lambda i: step(), args.steps)
+        rt.sync()
+        reps_lse = [timed(lambda i: step(), args.steps) for _ in range(max(1, args.reps // 2))]
+        k_lse = None
+        if not args.no_kernel_pass:
+            n_ev = 2 * len(kernels)
+            evs = [[hip.event() for _ in range(n_ev)] for _ in range(args.steps)]
+            ev_arrays = [(ctypes.c_void_p * n_ev)(*e) for e in evs]
+            for i in range(args.steps):
+                lib.gptc_set_kernel_events(ev_arrays[i], n_ev)
+                step()
+            rt.sync()
+            hip.device_sync()
+            lib.gptc_set_kernel_events(None, 0)
+            k_lse = {name: round(statistics.median(hip.elapsed_ms(e[2 * j], e[2 * j + 1]) for e in evs), 5)
+                     for j, name in enumerate(kernels)}
+        step()
+        rt.sync()
+        if not args.no_cpu_baseline:
+            lse_out = {"y": rt.to_numpy(yt), "lse": rt.to_numpy(caches[2]).reshape(B, H, T),
+                       "dqkv": rt.to_numpy(dqkv)}
+        lib.gptc_attention_set_state_limit(prev_limit)
+        t_lse = 6 * contraction_flops(B, T, H, D) / (ms_lse * 1e-3) / 1e12
+        lse_res = {
+            "ms_per_step": round(ms_lse, 5), "tflops": round(t_lse, 3),
+            "reps_ms_per_step": {"n": len(reps_lse), "median": round(statistics.median(reps_lse), 5),
+                                 "min": round(min(reps_lse), 5), "max": round(max(reps_lse), 5)},
+            "kernel_ms": k_lse,
+            "state_floats": lib.gptc_attention_state_floats(B, T, C, H),
+            "note": ("the forward keeps only the log-sum-exp (O(T) per head); the dk/dv kernel recomputes P from it "
+                     "(S, dP, dV, dK: 4 contractions) and writes dS to a scratch the dq kernel reads (1 contraction); "
+                     "kernel_ms keys as in the headline, dkdv = attn_bwd_dkdv_dma_kernel<RECOMP>"),
+        }
+        log(f"[bench] LSE-only state: {ms_lse:.4f} ms/step, {t_lse:.2f} TFLOP/s; kernels (ms): {k_lse}")
+
     step()  # leave the headline buffers with one fwd+bwd of the seeded inputs
     rt.sync()
 
@@ -758,17 +916,26 @@ def attention_bench(args):
                                           f"x{tr['fetch_scale']:.2f} + WRITE_SIZE x{tr['write_scale']:.2f})")
         result["roofline"] = roof
 
-    gpu_out = None
+    gpu_outs = None
     if not args.no_cpu_baseline:
-        gpu_out = {"y": rt.to_numpy(yt), "lse": rt.to_numpy(caches[2]).reshape(B, H, T),
-                   "dqkv": None if fwd_only else rt.to_numpy(dqkv)}
+        gpu_outs = {"default": {"y": rt.to_numpy(yt), "lse": rt.to_numpy(caches[2]).reshape(B, H, T),
+                                "dqkv": None if fwd_only else rt.to_numpy(dqkv)}}
+        if lse_out is not None:
+            gpu_outs["lse_only"] = lse_out
     for t in (dyt, mask, yt, dqkv, caches[0], caches[2], caches[3]):
         rt.free(t)
     rt.sync()
 
+    if lse_res is not None:
+        lse_res["pct_fp32_mfma_peak"] = round(100.0 * lse_res["tflops"] / peak, 2)
+        result["lse_only"] = lse_res
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle over OpenBLAS) ...")
-        cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s, gpu_out)
+        cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s, gpu_outs)
+        errs = cb.pop("gpu_max_abs_err")
+        cb["gpu_max_abs_err"] = errs.get("default")
+        if lse_res is not None:
+            lse_res["gpu_max_abs_err"] = errs.get("lse_only")
         result["cpu_baseline"] = {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cb.items()}
     else:
         result["cpu_baseline"] = None
@@ -785,6 +952,8 @@ def main():
                     help="copy: HBM copy of known size, to calibrate rocprof byte counters; "
                          "decode: the C4 KV-cache decode step; gpt2: the C3 GPT-2 124M training step; "
                          "c4: C4 greedy generation with GPT-2 124M")
+    ap.add_argument("--decode-layers", type=int, default=12,
+                    help="decode workload: layers whose caches each position runs through (GPT-2 small: 12)")
     ap.add_argument("--c4-loops", default="eager,graph,window",
                     help="c4 workload: the loops to time (comma list of eager, graph, window)")
     ap.add_argument("--reps", type=int, default=10,

@@ -3,11 +3,15 @@
 // Replaces kernels/src/cuda/Attention.cu:170-324 behind the signatures of
 // kernels/src/cuda/Attention.h:9-22 (called by
 // kernels/src/core/Attention.c:40-41,75-76).
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <initializer_list>
 #include <mutex>
+#include <vector>
+#include <tuple>
+#include <set>
 #include "attn_kernels.hpp"
 #include "ops_common.hpp"
 #include "gpu_kernels.h"
@@ -38,11 +42,15 @@ bool full_tiles(const Dims &d, std::initializer_list<uint32_t> strides) {
     return true;
 }
 
+// Head sizes 1 .. 128 run the MFMA kernels, 129 .. kGenericMaxD the generic
+// ones (plain FMAs, the LSE-only state); larger ones are refused.
+bool generic_head(const Dims &d) { return d.D > 2 * gptc::kDPad; }
+
 void check_head_size(const Dims &d) {
     CHECK_ERROR(d.H <= 0 || d.C % d.H != 0, "Expected C = %d to be divisible by n_heads = %d.", d.C, d.H);
-    CHECK_ERROR(d.D < 1 || d.D > 2 * gptc::kDPad,
+    CHECK_ERROR(d.D < 1 || d.D > gptc::kGenericMaxD,
                 "Head size %d is not supported by the GPU attention kernels (1 <= n_embd / n_heads <= %d).", d.D,
-                2 * gptc::kDPad);
+                gptc::kGenericMaxD);
 }
 
 // Views of q, k, v inside a (B, T, 3C) qkv tensor.
@@ -117,10 +125,17 @@ StateLayout state_layout(const Dims &d, bool reference_layout, bool lse_only) {
 // is the int length of a tensor_t, past which the state cannot exist.
 std::atomic<long long> g_state_limit{INT32_MAX};
 
+// Largest dS scratch (floats) the backward of the LSE-only state allocates
+// (in whole heads: chunks of as many heads as fit run one after the other).
+// The default, 2^30 floats (4 GiB), keeps the block offsets within 32 bits.
+constexpr long long kScratchLimitMax = 1LL << 30;
+std::atomic<long long> g_scratch_limit{kScratchLimitMax};
+
 // The state layout a forward uses: LSE-only when the D == 64 kernels run
-// (`full`) and the P' state would exceed the limit.
+// (`full`) and the P' state would exceed the limit, and always for the
+// generic head sizes.
 StateLayout forward_state(const Dims &d, bool reference_layout, bool full, bool *lse_only) {
-    *lse_only = full && state_layout(d, reference_layout, false).total > g_state_limit.load();
+    *lse_only = generic_head(d) || (full && state_layout(d, reference_layout, false).total > g_state_limit.load());
     const StateLayout s = state_layout(d, reference_layout, *lse_only);
     CHECK_ERROR(s.total > INT32_MAX,
                 "Attention state of %lld floats for B=%d, T=%d, H=%d exceeds the int length of a tensor_t "
@@ -139,6 +154,62 @@ void ensure_state_tensor(tensor_t *t, int64_t n) {
     t->length = static_cast<int>(n);
     for (int i = 0; i < 8; i++) t->shape[i] = 0;
     t->shape[0] = static_cast<int>(n);
+}
+
+// The mask.  gpt.c keeps score (i, j) where mask[i][j] == 1.0f and sets it
+// to -inf elsewhere (kernels/src/cpu/Attention.c:135-142, row stride the
+// mask's last dim).  The kernels apply the causal rule j <= i from indices
+// and never read the mask, so a mask that is not that rule on the T x T
+// block a call reads is refused.  The check reads the block once per mask
+// buffer and remembers it while the buffer's allocation serial is unchanged
+// (a new allocation at the same address, or a write into it through the
+// library's tensor data ops, checks again); a buffer that is not an
+// alloc_cuda block is checked at every call.  Writes by other kernels into
+// a checked mask are not seen.
+struct MaskKey {
+    const float *p;
+    uint64_t serial;
+    int T, stride;
+    bool operator<(const MaskKey &o) const {
+        return std::tie(p, serial, T, stride) < std::tie(o.p, o.serial, o.T, o.stride);
+    }
+};
+std::mutex g_mask_mu;
+std::set<MaskKey> g_causal_masks;
+
+void check_causal_mask(const tensor_t *mask, int T) {
+    const int stride = mask->shape[mask->ndims - 1];
+    const bool on_device = mask->device == CUDA;
+    const uint64_t serial = on_device ? gptc_block_serial(mask->t) : 0;
+    const MaskKey key{mask->t, serial, T, stride};
+    if (serial != 0) {
+        std::lock_guard<std::mutex> lk(g_mask_mu);
+        if (g_causal_masks.count(key)) return;
+    }
+    std::vector<float> m(static_cast<size_t>(T) * T);
+    if (on_device) {
+        hipStream_t s = gptc_stream_checked();
+        hipCheck(hipMemcpy2DAsync(m.data(), static_cast<size_t>(T) * sizeof(float), mask->t,
+                                  static_cast<size_t>(stride) * sizeof(float), static_cast<size_t>(T) * sizeof(float),
+                                  T, hipMemcpyDeviceToHost, s));
+        hipCheck(hipStreamSynchronize(s));
+    } else {
+        for (int i = 0; i < T; i++)
+            std::copy(mask->t + static_cast<size_t>(i) * stride, mask->t + static_cast<size_t>(i) * stride + T,
+                      m.begin() + static_cast<size_t>(i) * T);
+    }
+    for (int i = 0; i < T; i++)
+        for (int j = 0; j < T; j++) {
+            const bool keep = m[static_cast<size_t>(i) * T + j] == 1.0f;
+            CHECK_ERROR(keep != (j <= i),
+                        "The GPU attention kernels apply the causal mask (mask[i][j] == 1 exactly for j <= i); this "
+                        "mask differs at (%d, %d) (value %g).",
+                        i, j, (double)m[static_cast<size_t>(i) * T + j]);
+        }
+    if (serial != 0) {
+        std::lock_guard<std::mutex> lk(g_mask_mu);
+        g_causal_masks.insert(key);
+    }
 }
 
 // Events registered by gptc_set_kernel_events: [0,1] around the forward
@@ -188,9 +259,11 @@ void forward_impl(const tensor_t *input, const tensor_t *bias, const tensor_t *m
     const int mrows = mask->shape[mask->ndims - 2], mcols = mask->shape[mask->ndims - 1];
     CHECK_ERROR(mrows < d.T || mcols < d.T, "Sequence length T = %d exceeds the mask (block size %d x %d).", d.T,
                 mrows, mcols);
+    CHECK_ERROR(mask->t == NULL && d.T > 0, "Expected the mask to hold data.");
     CHECK_ERROR(output->length != d.B * d.T * d.C, "Expected output of %d elements, but got %d.", d.B * d.T * d.C,
                 output->length);
     if (d.B == 0 || d.T == 0 || d.C == 0) return;
+    check_causal_mask(mask, d.T);
 
     FwdParams p{};
     qkv_views(input->t, d, p.q, p.k, p.v);
@@ -340,9 +413,13 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
     p.delta = cache[3]->t + st.delta;
     // The backward consumes the state: dS overwrites P' (gpt.c's CPU backward
     // likewise reuses its caches as scratch, kernels/src/cpu/Attention.c:198-201).
-    // The LSE-only state has neither: both gradient kernels recompute P.
+    // The LSE-only state has neither: the dk/dv kernel recomputes P, and dS
+    // goes to a scratch of the packed blocks (below) for as many heads at a
+    // time as the scratch limit allows; without room for one head, the dq
+    // kernel recomputes P and dP as well.
     p.pm = lse_only ? nullptr : cache[3]->t + st.m;
     p.ds = lse_only ? nullptr : cache[3]->t + st.p;
+    p.lse_only = lse_only;
     p.dout = btc_view<HeadView>(static_cast<const float *>(global_grad->t), d);
     const uint32_t sb3 = static_cast<uint32_t>(d.T) * 3 * d.C, st3 = 3 * d.C;
     p.dq = HeadViewW{dout->t, sb3, st3, static_cast<uint32_t>(d.D)};
@@ -361,10 +438,22 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
     p.vec = (d.D % 4 == 0) && aligned16(p.q.p) && aligned16(p.k.p) && aligned16(p.v.p) && aligned16(y_saved) &&
             aligned16(global_grad->t) && aligned16(dout->t);
     p.full = p.vec && full_tiles(d, {p.q.st, p.k.st, p.dout.st});
-    CHECK_ERROR(lse_only && !p.full,
+    CHECK_ERROR(lse_only && !p.full && !generic_head(d),
                 "The forward kept the log-sum-exp-only state, which only the D = 64 kernels read, but these "
                 "gradient buffers need the other kernels (unaligned rows).");
     hipStream_t s = gptc_stream_checked();
+    float *ds_scratch = nullptr;
+    if (lse_only && p.full) {
+        const int64_t bh = static_cast<int64_t>(d.B) * d.H;
+        const int64_t per_head = static_cast<int64_t>(gptc::bwd_ds_floats(1, 1, d.T));
+        const int64_t heads = std::min<int64_t>(bh, g_scratch_limit.load() / per_head);
+        // Short heads (one recomputing workgroup per key block over all heads) take the scratch only whole.
+        if (heads >= 1 && (p.nqt > gptc::kShortHeadTiles || heads == bh)) {
+            ds_scratch = static_cast<float *>(alloc_cuda(static_cast<size_t>(heads * per_head) * sizeof(float)));
+            p.ds = ds_scratch;
+            p.ds_heads = static_cast<int>(heads);
+        }
+    }
     gptc::bwd_split_plan(p, s);
     bool folded = false;
     if (bias != nullptr) {
@@ -389,6 +478,9 @@ void backward_impl(const tensor_t *global_grad, tensor_t **cache, const tensor_t
         }
     }
     gptc::launch_attn_bwd(p, s, g_have_events ? g_events + 2 : nullptr);
+    // Stream-ordered: the block returns to the allocator's cache behind the
+    // kernels that use it.
+    if (ds_scratch != nullptr) free_cuda(ds_scratch);
     if (bias != nullptr) {
         const int nqt = (d.T + 63) / 64, nkb = (d.T + 127) / 128;
         if (folded) {
@@ -429,6 +521,10 @@ extern "C" long long gptc_attention_state_floats(int B, int T, int C, int n_head
 
 extern "C" long long gptc_attention_set_state_limit(long long floats) {
     return g_state_limit.exchange(floats < 0 ? static_cast<long long>(INT32_MAX) : floats);
+}
+
+extern "C" long long gptc_attention_set_scratch_limit(long long floats) {
+    return g_scratch_limit.exchange(floats < 0 || floats > kScratchLimitMax ? kScratchLimitMax : floats);
 }
 
 namespace {
@@ -495,7 +591,7 @@ void decode_step(const tensor_t *qkv, tensor_t *k_cache, tensor_t *v_cache, cons
     // allocator; the merge kernel reads it before anything queued later can
     // reuse it.
     bool own_part = false;
-    if (p.full) {
+    if (p.full && !gptc::dec_head_fits(p)) {
         if (part == nullptr) {
             part = static_cast<float *>(
                 alloc_cuda(static_cast<size_t>(p.B) * p.H * p.splits * gptc::kDecPartStride * sizeof(float)));
@@ -521,8 +617,10 @@ extern "C" void attention_decode_cuda_kernel(const tensor_t *qkv, tensor_t *k_ca
 // holds its own copy of the array until the process ends; host code reaches
 // it only through the address hipGetSymbolAddress returns for the current
 // device (the array's name is a host-side stand-in, not a device address).
-// Every call on a GPU reuses that GPU's array: calls that overlap on one GPU
-// (other streams, other threads) race.  Nothing needs clearing between
+// Steps of at most kDecHeadKeys keys run the one-launch kernel, which needs
+// no partials, so only longer steps use the array.  Every call on a GPU
+// reuses that GPU's array: calls that overlap on one GPU (other streams,
+// other threads) race.  Nothing needs clearing between
 // calls: the merge kernel reads only the partials the split kernel of the
 // same call wrote.
 namespace {
@@ -557,7 +655,7 @@ extern "C" void attention_decode_noalloc_cuda_kernel(const tensor_t *qkv, tensor
                                                      const int pos, const int n_heads, tensor_t *output) {
     gptc::DecParams p = decode_params(qkv, k_cache, v_cache, pos, nullptr, n_heads, output);
     if (p.B == 0 || p.C == 0) return;
-    if (p.full) {
+    if (p.full && !gptc::dec_head_fits(p)) {
         const size_t need = static_cast<size_t>(p.B) * p.H * p.splits * gptc::kDecPartStride;
         CHECK_ERROR(need > kDecodeScratchFloats,
                     "attention_decode_noalloc_cuda_kernel: B=%d, H=%d, pos=%d needs %zu floats of partials, more than "

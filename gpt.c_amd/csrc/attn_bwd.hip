@@ -232,7 +232,7 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
     // lane offset, so that every row of the half is an immediate offset.
     const uint32_t lane_off = 4 * hf * 32 + l32;
     auto half_base = [&](int qt, int qb) {
-        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh, n_qt, qt, kw0 >> 5)) + 32 * qb * 32);
+        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(bh - a.ds_bh0, n_qt, qt, kw0 >> 5)) + 32 * qb * 32);
     };
     auto load_p = [&](int qt, int qb) {
         if (RECOMP || !half_needed(qt, qb)) return;
@@ -439,18 +439,27 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
 // BIAS: the v bias joins the V rows as they are loaded; the q bias is added
 // to the Q operand of dK += dS^T Q as it is read (the same sum as adding it
 // to the stored tile: rows past T then hold the bias, with dS = 0 there).
-template <bool BIAS>
+//
+// RECOMP (the LSE-only state: the forward stored no P'): P is recomputed as
+// exp2(S log2(e)/sqrt(D) - LSE log2(e)) with S = Q K^T formed like dP (Q
+// rows from LDS as A operands, this lane's K row in registers as B
+// operands), and dS goes to a.ds, a scratch of the packed blocks of heads
+// [ds_bh0, ...) that the dq16 kernel reads next.  The Q tile is then stored
+// by rows, like dO (S reads a lane's query row as float4s; dK's B operand
+// becomes one word per MFMA, as dV's), and the statistics are the LSE (log2
+// units, +inf past T) and delta.
+template <bool BIAS, bool RECOMP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 attn_bwd_dkdv_dma_kernel(const BwdParams a) {
     constexpr int LS = kDPad + 4;      // LDS row stride (floats)
     constexpr int NJ = kDPad / 8;      // reduction steps of 8 dims (4 per lane half)
     constexpr int kTile = kBwdBQ * LS;      // floats per dO tile (rows)
-    constexpr int kQTile = kBwdBQ * kDPad;  // floats per Q tile ([q / 4][dim][q % 4])
+    constexpr int kQTile = RECOMP ? kTile : kBwdBQ * kDPad;  // floats per Q tile (rows, or [q / 4][dim][q % 4])
     __shared__ __attribute__((aligned(16))) float q_lds[2 * kQTile];
     __shared__ __attribute__((aligned(16))) float do_lds[2 * kTile];
     // Per buffer, one entry per thread: [0, 128) the factors f of P = P' * f
-    // for the workgroup's two 64-key tiles ([key tile][query]), [128, 192)
-    // delta, [192, 256) unused.
+    // for the workgroup's two 64-key tiles ([key tile][query]; RECOMP: [0, 64)
+    // LSE log2(e), +inf past T), [128, 192) delta, [192, 256) unused.
     __shared__ __attribute__((aligned(16))) float stat_lds[2 * 256];
     __shared__ float red_lds[4][2 * kDPad];
 
@@ -485,11 +494,16 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         h = bh - b * a.H;
     };
 
-    // V row of this lane's key, dims 8j + 4hf + c: B operand of dP = dO V^T.
-    // BIAS: the v bias joins it (keys past T keep a zero row); qbias holds
-    // the q bias of this lane's two dims.
+    // V row of this lane's key, dims 8j + 4hf + c: B operand of dP = dO V^T
+    // (RECOMP: the K row too, B operand of S = Q K^T).  BIAS: the v (and k)
+    // bias joins it (keys past T keep a zero row); qbias holds the q bias of
+    // this lane's two dims.
     f32x4 vr[NJ];
+    f32x4 kr[RECOMP ? NJ : 1];
     float qbias[2] = {0.0f, 0.0f};
+    // RECOMP with BIAS: S = (Q + qb) K'^T = Q K'^T + qb . K' (K' = K + kb):
+    // the q bias adds qbk = qb . K'[my_k] to every score of this lane's key.
+    float qbk = 0.0f;
     auto load_v = [&](const Step &s) {
         int b, h;
         head_of(s.bh, b, h);
@@ -498,10 +512,29 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         const float *Vh = a.v.p + b * a.v.sb + h * a.v.sh;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) vr[j] = k_ok ? load4<true>(Vh + my_k * a.v.st, 8 * j + 4 * hf, kDPad) : zero4();
+        if (RECOMP) {
+            const float *Kh = a.k.p + b * a.k.sb + h * a.k.sh;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                kr[j] = k_ok ? load4<true>(Kh + my_k * a.k.st, 8 * j + 4 * hf, kDPad) : zero4();
+        }
         if (BIAS) {
             if (k_ok) {
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) vr[j] += *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 8 * j + 4 * hf);
+                for (int j = 0; j < NJ; ++j) {
+                    vr[j] += *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + 8 * j + 4 * hf);
+                    if (RECOMP) kr[j] += *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + 8 * j + 4 * hf);
+                }
+            }
+            if (RECOMP) {
+                float part = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const f32x4 q4 = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 8 * j + 4 * hf);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) part = fmaf(q4[c], kr[j][c], part);
+                }
+                qbk = part + other_half(part);
             }
             qbias[0] = a.qb[h * kDPad + l32];
             qbias[1] = a.qb[h * kDPad + 32 + l32];
@@ -516,7 +549,8 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
     const uint32_t vl = 4u * lane;
     const uint32_t vq = 4u * ((lane & 3) * a.q.st + (lane >> 2));
     const uint32_t lds_q = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-                               (__attribute__((address_space(3))) float *)q_lds)) + 16u * w * kDPad * 4u);
+                               (__attribute__((address_space(3))) float *)q_lds)) +
+                           16u * w * (RECOMP ? LS : kDPad) * 4u);
     const uint32_t lds_do = uniform(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
                                 (__attribute__((address_space(3))) float *)do_lds)) + 16u * w * LS * 4u);
     auto load_tile = [&](const Step &s, int buf) {
@@ -530,8 +564,13 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         for (int i = 0; i < 16; ++i) {
             const uint32_t q = q0 + i;
             const uint32_t gq = q0 + 4 * (i >> 2);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rows, lds_ptr(mq + (i >> 2) * (4u * kDPad * 4u) + (i & 3) * 256u),
-                                                     4, gq * a.q.st * 4u + (i & 3) * 64u + vq, 0, 0, 0);
+            if (RECOMP)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rows, lds_ptr(mq + i * LS * 4u), 4, q * a.q.st * 4u + vl, 0,
+                                                         0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rows,
+                                                         lds_ptr(mq + (i >> 2) * (4u * kDPad * 4u) + (i & 3) * 256u),
+                                                         4, gq * a.q.st * 4u + (i & 3) * 64u + vq, 0, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(do_rows, lds_ptr(md + i * LS * 4u), 4,
                                                      q * a.dout.st * 4u + vl, 0, 0, 0);
         }
@@ -543,10 +582,15 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         const uint32_t bh = static_cast<uint32_t>(s.bh);
         const int q = s.qt * kBwdBQ + (tid & (kBwdBQ - 1));
         const int qc = min(q, T - 1);
-        const bool is_m = tid < 2 * kBwdBQ;
-        const int kt = 2 * s.kb + ((tid >> 6) & 1);
-        st_ok = q < T && (!is_m || kt < n_qt);
-        st0 = *(is_m ? a.pm + bh * n_qt * T + min(kt, n_qt - 1) * T + qc : a.delta + bh * T + qc);
+        if (RECOMP) {
+            st_ok = q < T;
+            st0 = a.delta[bh * T + qc];
+        } else {
+            const bool is_m = tid < 2 * kBwdBQ;
+            const int kt = 2 * s.kb + ((tid >> 6) & 1);
+            st_ok = q < T && (!is_m || kt < n_qt);
+            st0 = *(is_m ? a.pm + bh * n_qt * T + min(kt, n_qt - 1) * T + qc : a.delta + bh * T + qc);
+        }
         st1 = a.lse[bh * T + qc];
     };
 
@@ -558,10 +602,11 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
     const uint32_t lane_off = 4 * hf * 32 + l32;
     auto half_base = [&](const Step &s, int qb) {
         const int kw0 = s.kb * kBwdBK + 32 * w;
-        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(s.bh, n_qt, s.qt, kw0 >> 5)) + 32 * qb * 32);
+        return a.ds + uniform(static_cast<uint32_t>(ds_block_offset(s.bh - a.ds_bh0, n_qt, s.qt, kw0 >> 5)) +
+                              32 * qb * 32);
     };
     auto load_p = [&](const Step &s, int qb) {
-        if (!half_needed(s, qb)) return;
+        if (RECOMP || !half_needed(s, qb)) return;
         const float *hb = half_base(s, qb);
 #pragma unroll
         for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
@@ -646,7 +691,9 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
             default: __builtin_amdgcn_s_setprio(3); break;
         }
         ++done_steps;
-        {
+        if (RECOMP) {
+            stat_lds[buf * 256 + tid] = tid < kBwdBQ ? (st_ok ? st1 * kLog2e : INFINITY) : (st_ok ? st0 : 0.0f);
+        } else {
             const float f = fast_exp2(st0 - st1 * kLog2e);
             stat_lds[buf * 256 + tid] = st_ok ? (tid < 2 * kBwdBQ ? f : st0) : 0.0f;
         }
@@ -673,11 +720,37 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
 #pragma unroll
                     for (int c = 0; c < 4; ++c) dp = mfma32(da[c], vr[j][c], dp);
                 }
+                if (RECOMP) {
+                    // S (queries x keys), then P with the causal mask (keys
+                    // past T see only queries below T: masked too).
+                    s = zero16();
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x4 f4 = *reinterpret_cast<const f32x4 *>(&f_w[32 * qb + 8 * g + 4 * hf]);
+                    for (int j = 0; j < NJ; ++j) {
+                        const f32x4 qa = *reinterpret_cast<const f32x4 *>(&qs[(32 * qb + l32) * LS + 8 * j + 4 * hf]);
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) s[4 * g + c] = pbuf[4 * g + c] * f4[c];  // P
+                        for (int c = 0; c < 4; ++c) s = mfma32(qa[c], kr[j][c], s);
+                    }
+                    const float c2 = a.scale * kLog2e;
+                    const int my_k = cur.kb * kBwdBK + 32 * w + l32;
+                    const float *lse_w = stat_lds + buf * 256;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lse_w[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const int q = cur.qt * kBwdBQ + 32 * qb + 8 * g + 4 * hf + c;
+                            const float sv = BIAS ? s[4 * g + c] + qbk : s[4 * g + c];
+                            const float pv = fast_exp2(fmaf(sv, c2, -l4[c]));
+                            s[4 * g + c] = my_k > q ? 0.0f : pv;  // P
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 f4 = *reinterpret_cast<const f32x4 *>(&f_w[32 * qb + 8 * g + 4 * hf]);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) s[4 * g + c] = pbuf[4 * g + c] * f4[c];  // P
+                    }
                 }
             }
             if (qb == 0) {
@@ -703,16 +776,18 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
             for (int g = 0; g < 4; ++g) {
                 // Q rows 32qb + 8g + 4hf + c, c = 0..3, dim 32db + l32.
                 f32x4 q4[2];
+                if (!RECOMP) {
 #pragma unroll
-                for (int db = 0; db < 2; ++db)
-                    q4[db] = *reinterpret_cast<const f32x4 *>(&qs[(8 * qb + 2 * g + hf) * (4 * kDPad) +
-                                                                   (32 * db + l32) * 4]);
+                    for (int db = 0; db < 2; ++db)
+                        q4[db] = *reinterpret_cast<const f32x4 *>(&qs[(8 * qb + 2 * g + hf) * (4 * kDPad) +
+                                                                       (32 * db + l32) * 4]);
+                }
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int row = 32 * qb + 8 * g + 4 * hf + c;
 #pragma unroll
                     for (int db = 0; db < 2; ++db) {
-                        const float qv = q4[db][c];
+                        const float qv = RECOMP ? qs[row * LS + 32 * db + l32] : q4[db][c];
                         acc_dv[db] = mfma32(s[4 * g + c], dos[row * LS + 32 * db + l32], acc_dv[db]);
                         acc_dk[db] = mfma32(dp[4 * g + c], BIAS ? qv + qbias[db] : qv, acc_dk[db]);
                     }
@@ -903,7 +978,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
     auto prefetch_ds = [&](int hbh, int jq, int kt) {
         if (jq * kBwdBQ + 16 * w >= T) return;  // rows wholly past T: nothing to reduce
         const int nt = kt == jq ? w + 1 : 4;
-        const float *base = a.ds + uniform(static_cast<uint32_t>(ds_block_offset(hbh, nqt, jq, 2 * kt)));
+        const float *base = a.ds + uniform(static_cast<uint32_t>(ds_block_offset(hbh - a.ds_bh0, nqt, jq, 2 * kt)));
         const uint32_t off = (16 * w + n) * 32 + 4 * j;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -1223,10 +1298,15 @@ int bwd_split_plan(BwdParams &p, hipStream_t stream) {
     p.k_wg = 0;
     p.ksched = KeySched{nullptr, nullptr};
     if (!p.full || p.nqt <= kShortHeadTiles || p.ds == nullptr) return 0;  // the recomputing dk/dv runs whole blocks
-    // Both instances of the kernel keep two workgroups per CU; the lists are
+    // The LSE-only scratch in chunks of heads: no split blocks (their db
+    // partial rows would differ between chunks); the lists are built per
+    // chunk by launch_attn_bwd.
+    if (p.lse_only && p.ds_heads < p.B * p.H) return 0;
+    // Both instances of a kernel keep two workgroups per CU; the lists are
     // built for the residency of the one without the bias.
-    p.ksched = device_key_schedule(p.B * p.H, p.nqt, reinterpret_cast<const void *>(attn_bwd_dkdv_dma_kernel<false>),
-                                   stream, &p.k_wg, &p.nsplit);
+    const void *kernel = p.lse_only ? reinterpret_cast<const void *>(attn_bwd_dkdv_dma_kernel<false, true>)
+                                    : reinterpret_cast<const void *>(attn_bwd_dkdv_dma_kernel<false, false>);
+    p.ksched = device_key_schedule(p.B * p.H, p.nqt, kernel, stream, &p.k_wg, &p.nsplit);
     return p.nsplit;
 }
 
@@ -1263,12 +1343,55 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
         hipCheck(hipEventRecord(ev[1], stream));
         hipCheck(hipEventRecord(ev[2], stream));
     }
+    if (p.D > 2 * kDPad) {
+        launch_attn_bwd_generic(p, stream, ev);
+        if (ev) hipCheck(hipEventRecord(ev[5], stream));
+        return;
+    }
+    if (p.full && p.lse_only && p.ds != nullptr && p.nqt > kShortHeadTiles) {
+        // The LSE-only state with a dS scratch: per chunk of heads, dK/dV
+        // recomputing P (dS into the scratch), then dQ from that dS.  With
+        // more than one chunk the events bracket the whole loop as dk/dv.
+        const int BH = p.B * p.H;
+        const bool chunked = p.ds_heads < BH;
+        const void *kern = reinterpret_cast<const void *>(attn_bwd_dkdv_dma_kernel<false, true>);
+        for (int bh0 = 0; bh0 < BH; bh0 += p.ds_heads) {
+            const int nbh = std::min(p.ds_heads, BH - bh0);
+            BwdParams c = p;
+            c.ds_bh0 = bh0;
+            if (chunked) {
+                int ns = 0;
+                c.ksched = device_key_schedule(nbh, p.nqt, kern, stream, &c.k_wg, &ns, bh0, 0);
+                c.nsplit = 0;
+            }
+            if (c.qb != nullptr)
+                attn_bwd_dkdv_dma_kernel<true, true><<<dim3(c.k_wg), block, 0, stream>>>(c);
+            else
+                attn_bwd_dkdv_dma_kernel<false, true><<<dim3(c.k_wg), block, 0, stream>>>(c);
+            hipCheck(hipGetLastError());
+            if (ev && bh0 == 0 && !chunked) {
+                hipCheck(hipEventRecord(ev[3], stream));
+                hipCheck(hipEventRecord(ev[4], stream));
+            }
+            int num_wg = 0;
+            c.sched = device_block_schedule(nbh, p.nqt, reinterpret_cast<const void *>(attn_bwd_dq16_kernel), stream,
+                                            &num_wg, bh0);
+            attn_bwd_dq16_kernel<<<dim3(num_wg), block, 0, stream>>>(c);
+            hipCheck(hipGetLastError());
+        }
+        if (ev && chunked) {
+            hipCheck(hipEventRecord(ev[3], stream));
+            hipCheck(hipEventRecord(ev[4], stream));
+        }
+        if (ev) hipCheck(hipEventRecord(ev[5], stream));
+        return;
+    }
     if (p.full && (p.nqt <= kShortHeadTiles || p.ds == nullptr))
         attn_bwd_dkdv_kernel<true, true, true><<<grid_k, block, 0, stream>>>(p);
     else if (p.full && p.qb != nullptr)
-        attn_bwd_dkdv_dma_kernel<true><<<dim3(p.k_wg), block, 0, stream>>>(p);
+        attn_bwd_dkdv_dma_kernel<true, false><<<dim3(p.k_wg), block, 0, stream>>>(p);
     else if (p.full)
-        attn_bwd_dkdv_dma_kernel<false><<<dim3(p.k_wg), block, 0, stream>>>(p);
+        attn_bwd_dkdv_dma_kernel<false, false><<<dim3(p.k_wg), block, 0, stream>>>(p);
     else if (wide && p.vec)
         attn_bwd_dkdv_kernel<true, false, false, 2 * kDPad><<<grid_k, block, 0, stream>>>(p);
     else if (wide)

@@ -10,10 +10,13 @@
 // softmax(q k^T / sqrt(D)) v), reading each cached key and value once.
 //
 // The work is HBM- and latency-bound (4 L D flop against 8 L D bytes per
-// (b, h)).  For D == 64 with 16-byte cache rows the split-key kernels at the
-// end of this file run; the kernel first below serves the other head sizes:
+// (b, h)).  For D == 64 with 16-byte cache rows, steps of at most
+// kDecHeadKeys keys run attn_decode_head_kernel (one launch, one workgroup
+// per (b, h)) and longer ones the split-key pair at the end of this file;
+// the kernel first below serves the other head sizes:
 // one 1024-thread workgroup (16 waves) per (b, h), with as many row loads in
-// flight as the registers allow (head sizes up to 128).
+// flight as the registers allow (head sizes up to 128, and a build for the
+// generic head sizes up to kGenericMaxD).
 //   phase 1  thread per key: t_j = (q . k_j) log2(e)/sqrt(D) into LDS;
 //   phase 2  workgroup max m and sum l of p_j = exp2(t_j - m);
 //   phase 3  wave per key row, lane per dim: o = sum_j p_j v_j (coalesced
@@ -22,6 +25,8 @@
 #include "attn_common.hpp"
 #include "attn_kernels.hpp"
 #include "hip_check.hpp"
+
+#include <mutex>
 
 namespace gptc {
 
@@ -49,9 +54,12 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
 
 }  // namespace
 
-constexpr int kDecMaxD = 2 * kDPad;  // head sizes up to 128
-
+// DMAX: the largest head size of the build, 2 * kDPad (128) or kGenericMaxD
+// (1024, the generic head sizes; more LDS per workgroup).
+template <int DMAX>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecParams a) {
+    constexpr int kDecMaxD = DMAX;
+    static_assert(DMAX <= kDecThreads, "one thread per dim loads the new row");
     extern __shared__ float dyn_lds[];  // scores: pos + 1 floats (L with a device-side position)
     __shared__ float q_s[kDecMaxD], k_s[kDecMaxD], v_s[kDecMaxD];
     __shared__ float o_s[kDecWaves][kDecMaxD];
@@ -296,7 +304,135 @@ __global__ __launch_bounds__(64) void attn_decode_merge_kernel(const DecParams a
     a.out[static_cast<size_t>(b) * a.C + h * kDPad + d] = o / l;
 }
 
+// ---- One-launch decode of a short cache (D == 64, 16-byte rows) ----
+//
+// For up to kDecHeadKeys keys the whole (b, h) fits one 1024-thread
+// workgroup with every K and V row it needs in flight at once, so the step
+// is one launch and one memory round trip (the split pair above costs two
+// launches).  Key j of round r (j = 64r + 4w + lane/16) belongs to the 16
+// lanes of row group lane/16 of wave w; lane g = lane % 16 holds dims
+// 4g .. 4g+3 of that key's K and V rows.  Per lane: q[4g..4g+3], then the
+// dot products of its keys reduced over the 16 lanes of the group (each of
+// them then holds t_j), the workgroup max through LDS, p_j = exp2(t_j - m),
+// o = sum p_j v_j over the lane's keys, reduced over the wave's four groups
+// and the 16 waves (a fixed order), and y = o / l.  Key pos (the new token)
+// is read from the qkv row and written to both caches at pos.
+// R: the rounds of 64 keys that hold a key (pos / 64 + 1), a compile-time
+// count so that the loads of empty rounds are not issued at all (they would
+// still cost the CU's L1 bandwidth, the step's bound at B = 1).
+template <int R>
+__device__ __forceinline__ void decode_head_rounds(const DecParams &a, int pos, float *m_red, float *l_red,
+                                                   float (*o_red)[kDPad]) {
+    const int tid = threadIdx.x, lane = tid & 63, g = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bh = blockIdx.x;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int n = pos + 1;
+
+    const float *row = a.qkv + static_cast<size_t>(b) * 3 * a.C + h * kDPad;
+    float *kc = a.k_cache + static_cast<size_t>(bh) * a.L * kDPad;
+    float *vc = a.v_cache + static_cast<size_t>(bh) * a.L * kDPad;
+    const f32x4 q4 = *reinterpret_cast<const f32x4 *>(row + 4 * g);
+    // Every K and V row of this lane's keys, requested before any is used
+    // (no branch or select between the loads, which would wait for them):
+    // keys pos and beyond read the new row, whose k, v are finite; keys past
+    // pos get t = -inf and p = 0 below.
+    f32x4 k4[R], v4[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int j = 64 * r + 4 * w + (lane >> 4);
+        const size_t cj = static_cast<size_t>(j < pos ? j : 0) * kDPad;
+        const float *kr = j < pos ? kc + cj : row + a.C;
+        const float *vr = j < pos ? vc + cj : row + 2 * a.C;
+        k4[r] = *reinterpret_cast<const f32x4 *>(kr + 4 * g);
+        v4[r] = *reinterpret_cast<const f32x4 *>(vr + 4 * g);
+    }
+    if (tid < 16) {
+        // The new k, v into the caches at pos (read from the qkv row).
+        const f32x4 kn = *reinterpret_cast<const f32x4 *>(row + a.C + 4 * tid);
+        const f32x4 vn = *reinterpret_cast<const f32x4 *>(row + 2 * a.C + 4 * tid);
+        *reinterpret_cast<f32x4 *>(kc + static_cast<size_t>(pos) * kDPad + 4 * tid) = kn;
+        *reinterpret_cast<f32x4 *>(vc + static_cast<size_t>(pos) * kDPad + 4 * tid) = vn;
+    }
+
+    // Scores t_j (log2 units) of the lane's keys, -inf past pos.
+    float t[R];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc = q4[0] * k4[r][0];
+        acc = fmaf(q4[1], k4[r][1], acc);
+        acc = fmaf(q4[2], k4[r][2], acc);
+        acc = fmaf(q4[3], k4[r][3], acc);
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
+        const int j = 64 * r + 4 * w + (lane >> 4);
+        t[r] = j < n ? acc * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, t[r]);
+    }
+    // The four row groups of the wave, then the 16 waves.
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (lane == 0) m_red[w] = mx;
+    __syncthreads();
+    float m = m_red[0];
+#pragma unroll
+    for (int i = 1; i < kDecWaves; ++i) m = fmaxf(m, m_red[i]);
+
+    float l = 0.0f;
+    f32x4 o = zero4();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float p = fast_exp2(t[r] - m);  // 0 past pos
+        l += p;
+        o += p * v4[r];
+    }
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+        l += __shfl_xor(l, off, 64);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], off, 64);
+    }
+    if (lane < 16) *reinterpret_cast<f32x4 *>(&o_red[w][4 * lane]) = o;
+    if (lane == 0) l_red[w] = l;
+    __syncthreads();
+    if (tid < kDPad) {
+        float y = o_red[0][tid], ls = l_red[0];
+#pragma unroll
+        for (int i = 1; i < kDecWaves; ++i) {
+            y += o_red[i][tid];
+            ls += l_red[i];
+        }
+        a.out[static_cast<size_t>(b) * a.C + h * kDPad + tid] = y / ls;
+    }
+}
+
+__global__ __launch_bounds__(kDecThreads) void attn_decode_head_kernel(const DecParams a) {
+    static_assert(kDecHeadKeys == 8 * 64, "the switch below covers 8 rounds of 64 keys");
+    __shared__ float m_red[kDecWaves];
+    __shared__ float l_red[kDecWaves];
+    __shared__ __attribute__((aligned(16))) float o_red[kDecWaves][kDPad];
+
+    const int pos = a.pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*a.pos_dev) : a.pos;
+    if (pos < 0 || pos >= a.L || pos >= kDecHeadKeys) return;
+    switch (pos >> 6) {  // uniform
+        case 0: decode_head_rounds<1>(a, pos, m_red, l_red, o_red); break;
+        case 1: decode_head_rounds<2>(a, pos, m_red, l_red, o_red); break;
+        case 2: decode_head_rounds<3>(a, pos, m_red, l_red, o_red); break;
+        case 3: decode_head_rounds<4>(a, pos, m_red, l_red, o_red); break;
+        case 4: decode_head_rounds<5>(a, pos, m_red, l_red, o_red); break;
+        case 5: decode_head_rounds<6>(a, pos, m_red, l_red, o_red); break;
+        case 6: decode_head_rounds<7>(a, pos, m_red, l_red, o_red); break;
+        default: decode_head_rounds<8>(a, pos, m_red, l_red, o_red); break;
+    }
+}
+
 void launch_attn_decode(const DecParams &p, hipStream_t stream) {
+    if (p.full && dec_head_fits(p)) {
+        attn_decode_head_kernel<<<dim3(p.B * p.H), dim3(kDecThreads), 0, stream>>>(p);
+        hipCheck(hipGetLastError());
+        return;
+    }
     if (p.full && p.part != nullptr) {
         attn_decode_split_kernel<<<dim3(p.B * p.H * p.splits), dim3(256), 0, stream>>>(p);
         hipCheck(hipGetLastError());
@@ -305,7 +441,16 @@ void launch_attn_decode(const DecParams &p, hipStream_t stream) {
         return;
     }
     const size_t lds = static_cast<size_t>(p.pos_dev != nullptr ? p.L : p.pos + 1) * sizeof(float);
-    attn_decode_kernel<<<dim3(p.B * p.H), dim3(kDecThreads), lds, stream>>>(p);
+    if (p.D <= 2 * kDPad) {
+        attn_decode_kernel<2 * kDPad><<<dim3(p.B * p.H), dim3(kDecThreads), lds, stream>>>(p);
+    } else {
+        static std::once_flag once;
+        std::call_once(once, [] {
+            hipCheck(hipFuncSetAttribute(reinterpret_cast<const void *>(attn_decode_kernel<kGenericMaxD>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kDecMaxKeys * sizeof(float)));
+        });
+        attn_decode_kernel<kGenericMaxD><<<dim3(p.B * p.H), dim3(kDecThreads), lds, stream>>>(p);
+    }
     hipCheck(hipGetLastError());
 }
 

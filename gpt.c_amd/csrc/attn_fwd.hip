@@ -248,7 +248,7 @@ attn_fwd_kernel(const FwdParams a) {
 // own keys, where block NKB - 1 is masked per key).
 //
 // Scores: S^T = K Q^T on 16 x 16 x 4 (Q^T in registers, qr[c][e] = Q[my_q]
-// [16g + 4c + e]), the tile's row maximum (log2 units), the online softmax
+// [16c + 4g + e]), the tile's row maximum (log2 units), the online softmax
 // with lazy rescaling (the running maximum moves only when a row maximum
 // grows by more than 2^kRescaleLog2), P' = exp2(S c2 - m_use) into sc and its
 // row sums into l_run.  Returns m_use (0 while the row is all masked).
@@ -303,13 +303,32 @@ __device__ __forceinline__ float fwd16_scores_op(KOp k_op, const f32x4 (&qr)[4],
     return m_use;
 }
 
+// LDS tiles of the 16-row forwards (64 keys x 64 dims each, no padding):
+//   K: the 16-byte chunk d / 4 of key k sits at chunk (d / 4) ^ (k % 16) of
+//     row k.  Lane group g of score step c reads dims 16c + 4g .. +3 of key
+//     i16 (the Q operands use the same dims), i.e. chunk (4c + g) ^ i16;
+//     a tile store (lanes 0..15 one row, one chunk each) writes one row's
+//     16 chunks in permuted order;
+//   V: row-major: lane (g, i16) reads row 4g + r at dims 4 i16, 256
+//     contiguous bytes per group, the groups 1 KB apart.
+// Measured with SQ_LDS_BANK_CONFLICT on gfx950 (an access-pattern probe of
+// each read and store): these four accesses show no bank conflicts.  The
+// rows of 68 floats used before, with dims 16g + 4c for lane group g,
+// conflicted on both reads (half of the forward's LDS-active cycles), and
+// so did K rows of 68 or 76 floats with dims 16c + 4g, and the XOR layout
+// with dims 16g + 4c.
+constexpr int kKStride = kDPad;
+constexpr int kVStride = kDPad;
+__device__ __forceinline__ int ktile_at(int key, int dim) {
+    return key * kKStride + ((((dim >> 2) ^ (key & 15)) << 2) | (dim & 3));
+}
+__device__ __forceinline__ int vtile_at(int key, int dim) { return key * kVStride + dim; }
+
 template <int NKB, bool DIAG>
 __device__ __forceinline__ float fwd16_scores(const float *k_t, const f32x4 (&qr)[4], int g, int i16, float c2,
                                               float &m_run, float &l_run, f32x4 (&acc)[4], f32x4 (&sc)[4]) {
     return fwd16_scores_op<NKB, DIAG>(
-        [&](int kb, int c) {
-            return *reinterpret_cast<const f32x4 *>(&k_t[(16 * kb + i16) * kLdsStride + 16 * g + 4 * c]);
-        },
+        [&](int kb, int c) { return *reinterpret_cast<const f32x4 *>(&k_t[ktile_at(16 * kb + i16, 16 * c + 4 * g)]); },
         qr, g, i16, c2, m_run, l_run, acc, sc);
 }
 
@@ -332,9 +351,7 @@ __device__ __forceinline__ void fwd16_pv_op(VOp v_op, const f32x4 (&sc)[4], f32x
 template <int NKB>
 __device__ __forceinline__ void fwd16_pv(const float *v_t, const f32x4 (&sc)[4], int g, int i16, f32x4 (&acc)[4]) {
     fwd16_pv_op<NKB>(
-        [&](int kb, int r) {
-            return *reinterpret_cast<const f32x4 *>(&v_t[(16 * kb + 4 * g + r) * kLdsStride + 4 * i16]);
-        },
+        [&](int kb, int r) { return *reinterpret_cast<const f32x4 *>(&v_t[vtile_at(16 * kb + 4 * g + r, 4 * i16)]); },
         sc, acc);
 }
 
@@ -363,8 +380,8 @@ constexpr int kF16Rows = 64;  // queries per block of the 16-row kernel (4 waves
 template <bool PERM, bool DEEP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEEP ? 2 : 3, DEEP ? 2 : 3))) void
 attn_fwd16_kernel(const FwdParams a) {
-    __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float k_lds[kFwdBN * kKStride];
+    __shared__ __attribute__((aligned(16))) float v_lds[kFwdBN * kVStride];
     // The qkv bias of the current step's head (q | k | v, 64 floats each).
     __shared__ __attribute__((aligned(16))) float bias_lds[3 * kDPad];
 
@@ -428,12 +445,12 @@ attn_fwd16_kernel(const FwdParams a) {
     int kt = 0, bh = sched_bh(a.sched.items[it]), jq = sched_j(a.sched.items[it]);
     int b = bh / a.H, h = bh - b * a.H;
     const float c2 = a.scale_log2;
-    f32x4 qr[4];  // Q[my_q][16g + 4c + e] in qr[c][e]: the B operand of step 4c + e
+    f32x4 qr[4];  // Q[my_q][16c + 4g + e] in qr[c][e]: the B operand of step 4c + e
     auto load_q = [&]() {
         const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
         const int q = jq * kF16Rows + 16 * w + i16;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * g + 4 * c);
+        for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * c + 4 * g);
     };
     load_q();
     load_tile(bh, 0, kpre, vpre, bpre);
@@ -477,9 +494,9 @@ attn_fwd16_kernel(const FwdParams a) {
             // for the first block, here for the others).
             if (it != it_first) load_q();
             if (PERM && my_q < T) {
-                float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * kDPad + 16 * g;
+                float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * kDPad + 4 * g;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) *reinterpret_cast<f32x4 *>(dst + 4 * c) = qr[c];
+                for (int c = 0; c < 4; ++c) *reinterpret_cast<f32x4 *>(dst + 16 * c) = qr[c];
             }
             m_run = -INFINITY;
             l_run = 0.0f;
@@ -519,9 +536,8 @@ attn_fwd16_kernel(const FwdParams a) {
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = ld_row + 16 * i;
-            *reinterpret_cast<f32x4 *>(&k_lds[row * kLdsStride + ld_col]) = kpre[i];
-            *reinterpret_cast<f32x4 *>(&v_lds[row * kLdsStride + ld_col]) = vpre[i];
+            *reinterpret_cast<f32x4 *>(&k_lds[ktile_at(ld_row + 16 * i, ld_col)]) = kpre[i];
+            *reinterpret_cast<f32x4 *>(&v_lds[vtile_at(ld_row + 16 * i, ld_col)]) = vpre[i];
         }
         const bool diag = kt == jq;  // the block's own keys: the last tile of the block
         if (PERM && diag) {
@@ -545,7 +561,7 @@ attn_fwd16_kernel(const FwdParams a) {
         }
         if (biased && kt == 0) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) qr[c] += *reinterpret_cast<const f32x4 *>(&bias_lds[16 * g + 4 * c]);
+            for (int c = 0; c < 4; ++c) qr[c] += *reinterpret_cast<const f32x4 *>(&bias_lds[16 * c + 4 * g]);
         }
 
         if (!diag) {
@@ -599,9 +615,9 @@ attn_fwd16_kernel(const FwdParams a) {
 // recomputes P, so no P' or m is stored.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 attn_fwd_short_kernel(const FwdParams a) {
-    constexpr int TILE = kFwdBN * kLdsStride;
-    __shared__ __attribute__((aligned(16))) float k_lds[kShortHeadTiles * TILE];
-    __shared__ __attribute__((aligned(16))) float v_lds[kShortHeadTiles * TILE];
+    constexpr int KTILE = kFwdBN * kKStride, VTILE = kFwdBN * kVStride;
+    __shared__ __attribute__((aligned(16))) float k_lds[kShortHeadTiles * KTILE];
+    __shared__ __attribute__((aligned(16))) float v_lds[kShortHeadTiles * VTILE];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -617,9 +633,9 @@ attn_fwd_short_kernel(const FwdParams a) {
     const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
     const auto k_rows = head_rows(a.k.p + b * a.k.sb + h * a.k.sh, T, a.k.st);
     const auto v_rows = head_rows(a.v.p + b * a.v.sb + h * a.v.sh, T, a.v.st);
-    f32x4 qr[4];  // Q[my_q][16g + 4c + e] in qr[c][e]
+    f32x4 qr[4];  // Q[my_q][16c + 4g + e] in qr[c][e]
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(my_q) * a.q.st + 16 * g + 4 * c);
+    for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(my_q) * a.q.st + 16 * c + 4 * g);
     const int ld_row = tid >> 4, ld_col = 4 * (tid & 15);
     f32x4 kpre[kShortHeadTiles][4], vpre[kShortHeadTiles][4];
 #pragma unroll
@@ -643,16 +659,15 @@ attn_fwd_short_kernel(const FwdParams a) {
         kb4 = *reinterpret_cast<const f32x4 *>(a.kb + h * kDPad + ld_col);
         vb4 = *reinterpret_cast<const f32x4 *>(a.vb + h * kDPad + ld_col);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qb4[c] = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * g + 4 * c);
+        for (int c = 0; c < 4; ++c) qb4[c] = *reinterpret_cast<const f32x4 *>(a.qb + h * kDPad + 16 * c + 4 * g);
     }
 #pragma unroll
     for (int kt = 0; kt < kShortHeadTiles; ++kt)
         if (kt <= jq) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int row = ld_row + 16 * i;
-                *reinterpret_cast<f32x4 *>(&k_lds[kt * TILE + row * kLdsStride + ld_col]) = kpre[kt][i] + kb4;
-                *reinterpret_cast<f32x4 *>(&v_lds[kt * TILE + row * kLdsStride + ld_col]) = vpre[kt][i] + vb4;
+                *reinterpret_cast<f32x4 *>(&k_lds[kt * KTILE + ktile_at(ld_row + 16 * i, ld_col)]) = kpre[kt][i] + kb4;
+                *reinterpret_cast<f32x4 *>(&v_lds[kt * VTILE + vtile_at(ld_row + 16 * i, ld_col)]) = vpre[kt][i] + vb4;
             }
         }
 #pragma unroll
@@ -669,7 +684,7 @@ attn_fwd_short_kernel(const FwdParams a) {
         fwd16_scores<4, false>(k_lds, qr, g, i16, c2, m_run, l_run, acc, sc);
         fwd16_pv<4>(v_lds, sc, g, i16, acc);
     }
-    const float *k_d = k_lds + jq * TILE, *v_d = v_lds + jq * TILE;
+    const float *k_d = k_lds + jq * KTILE, *v_d = v_lds + jq * VTILE;
     switch (w) {  // wave-uniform: the 16-key blocks of the diagonal tile this wave sees
         case 0: fwd16_scores<1, true>(k_d, qr, g, i16, c2, m_run, l_run, acc, sc); fwd16_pv<1>(v_d, sc, g, i16, acc); break;
         case 1: fwd16_scores<2, true>(k_d, qr, g, i16, c2, m_run, l_run, acc, sc); fwd16_pv<2>(v_d, sc, g, i16, acc); break;
@@ -868,6 +883,12 @@ attn_fwd_twotile_kernel(const FwdParams a) {
 void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t *ev) {
     FwdParams p = p_in;
     const bool perm = p.qp != nullptr;
+    if (p.D > 2 * kDPad) {
+        if (ev) hipCheck(hipEventRecord(ev[0], stream));
+        launch_attn_fwd_generic(p, stream);
+        if (ev) hipCheck(hipEventRecord(ev[1], stream));
+        return;
+    }
     if (p.full) {
         // Short heads leave P' to the backward; in the compact layout they
         // run one workgroup per block, in the reference layout the DEEP

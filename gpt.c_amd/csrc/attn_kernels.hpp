@@ -94,6 +94,14 @@ struct BwdParams {
     int nsplit;
     KeySched ksched;
     int k_wg;  // workgroups of the work-list launch
+    // The LSE-only state (the forward kept no P'): with ds set, it is a
+    // scratch of the packed blocks of ds_heads heads at a time, which the
+    // recomputing dk/dv kernel fills with dS and the dq16 kernel reads; the
+    // heads run in chunks [ds_bh0, ds_bh0 + ds_heads) (ds_bh0 set per chunk
+    // by launch_attn_bwd).  ds == nullptr: both gradient kernels recompute P.
+    bool lse_only;
+    int ds_heads;
+    int ds_bh0;
 };
 
 // Sets p.nsplit, p.ksched and p.k_wg for the D = 64 dk/dv kernel of p's
@@ -121,6 +129,15 @@ constexpr int kDecMaxKeys = 8192;  // pos + 1 limit (the scores live in LDS)
 constexpr int kDecChunk = 64;      // keys per workgroup of the split-key decode
 constexpr int kDecPartStride = 68; // floats per partial: o[64], m, l, 2 unused
 
+constexpr int kDecHeadKeys = 512;  // keys the one-launch decode (one workgroup per (b, h)) takes
+
+// Whether a decode step runs the one-launch kernel: D == 64 with 16-byte
+// rows, and at most kDecHeadKeys keys (pos + 1, or the cache length L when
+// the position is read on the device).  Longer steps run the split pair.
+inline bool dec_head_fits(const DecParams &p) {
+    return p.full && (p.pos_dev != nullptr ? p.L : p.pos + 1) <= kDecHeadKeys;
+}
+
 // Floats of the partials buffer of the split-key decode for B sequences of
 // H heads attending up to n_keys keys.
 inline size_t dec_part_floats(int B, int H, int n_keys) {
@@ -135,5 +152,13 @@ void launch_attn_decode(const DecParams &p, hipStream_t stream);
 // nullptr: no events.
 void launch_attn_fwd(const FwdParams &p, hipStream_t stream, const hipEvent_t *ev);
 void launch_attn_bwd(const BwdParams &p, hipStream_t stream, const hipEvent_t *ev);
+
+// Head sizes past 2 * kDPad, up to kGenericMaxD: plain-FMA kernels
+// (attn_generic.hip) with the LSE-only state.  The backward launcher runs
+// the dk/dv and dq kernels (the delta kernel is launch_attn_bwd's) and
+// records ev[3], ev[4] between them.
+constexpr int kGenericMaxD = 1024;
+void launch_attn_fwd_generic(const FwdParams &p, hipStream_t stream);
+void launch_attn_bwd_generic(const BwdParams &p, hipStream_t stream, const hipEvent_t *ev);
 
 }  // namespace gptc

@@ -219,8 +219,20 @@ struct DeviceKeyTable {
 };
 
 std::mutex g_mu;
-std::map<std::tuple<int, int, int, int>, DeviceTable> g_tables;  // (device, BH, nqt, per_cu)
-std::map<std::tuple<int, int, int, int>, DeviceKeyTable> g_key_tables;  // (device, BH, nqt, per_cu)
+// (device, BH, nqt, per_cu * 1024 + cus, bh0[, max_split])
+std::map<std::tuple<int, int, int, int, int>, DeviceTable> g_tables;
+std::map<std::tuple<int, int, int, int, int, int>, DeviceKeyTable> g_key_tables;
+
+// The uploads below allocate and copy from host memory, which a stream under
+// graph capture cannot record: refuse with a clear message instead.
+void check_not_capturing(hipStream_t stream, const char *what) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    hipCheck(hipStreamIsCapturing(stream, &st));
+    CHECK_ERROR(st != hipStreamCaptureStatusNone,
+                "The %s of this attention shape is built on its first call, which must not be captured into a graph: "
+                "run one forward and backward of the shape before capturing.",
+                what);
+}
 std::map<std::pair<int, const void *>, std::pair<int, int>> g_occupancy;  // (device, kernel) -> (per_cu, cus)
 
 // (workgroups per CU, CUs per XCD) of `kernel` on device dev; g_mu held.
@@ -238,13 +250,14 @@ std::pair<int, int> occupancy_locked(int dev, const void *kernel) {
 
 }  // namespace
 
-KeyTable build_key_schedule(int BH, int nqt, int per_cu, int cus) {
+KeyTable build_key_schedule(int BH, int nqt, int per_cu, int cus, int max_split) {
     CHECK_ERROR(BH < 0 || nqt < 1 || per_cu < 1 || cus < 1, "key schedule: unsupported shape (heads %d, tiles %d, per CU %d, CUs %d).",
                 BH, nqt, per_cu, cus);
     const int nkb = (nqt + kKeyTilesPerBlock - 1) / kKeyTilesPerBlock;
+    const int ns_max = max_split < 0 ? nkb : std::min(max_split, nkb);
     std::vector<KeyTable> cand;
     double best = 0.0;
-    for (int ns = 0; ns <= nkb; ++ns) {
+    for (int ns = 0; ns <= ns_max; ++ns) {
         cand.push_back(key_schedule_with(BH, nqt, ns, per_cu, cus));
         best = ns == 0 ? cand.back().est : std::min(best, cand.back().est);
     }
@@ -266,17 +279,21 @@ SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus) {
     return best;
 }
 
-BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg) {
+BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int bh0) {
     int dev = 0;
     hipCheck(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_mu);
     const auto occ = occupancy_locked(dev, kernel);
     const int per_cu = occ.first, cus = occ.second;
-    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus);
+    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus, bh0);
     auto it = g_tables.find(key);
     if (it == g_tables.end()) {
+        check_not_capturing(stream, "work list");
+        CHECK_ERROR(static_cast<long long>(bh0) + BH >= (1LL << (31 - kSchedJBits)),
+                    "block schedule: head index %d beyond the work-list format.", bh0 + BH);
         DeviceTable d;
         d.host = build_block_schedule(BH, nqt, per_cu, cus);
+        for (int &item : d.host.items) item += bh0 << kSchedJBits;
         d.num_wg = d.host.num_wg;
         const size_t nw = d.host.wg_start.size() * sizeof(int), ni = std::max<size_t>(1, d.host.items.size()) * sizeof(int);
         hipCheck(hipMalloc(&d.wg_start, nw));
@@ -291,17 +308,20 @@ BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_
     return BlockSched{it->second.wg_start, it->second.items};
 }
 
-KeySched device_key_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int *nsplit) {
+KeySched device_key_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int *nsplit,
+                             int bh0, int max_split) {
     int dev = 0;
     hipCheck(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_mu);
     const auto occ = occupancy_locked(dev, kernel);
     const int per_cu = occ.first, cus = occ.second;
-    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus);
+    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus, bh0, max_split);
     auto it = g_key_tables.find(key);
     if (it == g_key_tables.end()) {
+        check_not_capturing(stream, "key-block work list");
         DeviceKeyTable d;
-        d.host = build_key_schedule(BH, nqt, per_cu, cus);
+        d.host = build_key_schedule(BH, nqt, per_cu, cus, max_split);
+        for (size_t i = 0; i < d.host.items.size(); i += 4) d.host.items[i] += bh0;
         d.num_wg = d.host.num_wg;
         d.nsplit = d.host.nsplit;
         const size_t nw = d.host.wg_start.size() * sizeof(int), ni = std::max<size_t>(1, d.host.items.size()) * sizeof(int);

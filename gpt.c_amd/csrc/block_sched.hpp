@@ -55,9 +55,12 @@ struct SchedTable {
 SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus);
 
 // The device copy of build_block_schedule(BH, nqt, per_cu of `kernel`) for
-// the current device, built and uploaded (stream-ordered on `stream`) on
-// first use and cached for the life of the process.
-BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg);
+// the current device, with bh0 added to every head index (the heads
+// [bh0, bh0 + BH) of a larger problem), built and uploaded (stream-ordered on
+// `stream`) on first use and cached for the life of the process.  The first
+// use of a shape must not happen while `stream` is being captured into a
+// graph (it allocates and copies from host memory): that is a fatal error.
+BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int bh0 = 0);
 
 // ---- Work lists of the D = 64 dk/dv kernel ----
 //
@@ -91,11 +94,13 @@ struct KeyTable {
     double est = 0.0;  // the estimated time the choice of nsplit minimised (tiles)
 };
 
-KeyTable build_key_schedule(int BH, int nqt, int per_cu, int cus);
+// max_split: the largest nsplit considered (-1: every count up to nkb).
+KeyTable build_key_schedule(int BH, int nqt, int per_cu, int cus, int max_split = -1);
 
 // The device copy of build_key_schedule for the current device and the
-// residency of `kernel`, built, uploaded (stream-ordered on `stream`) and
-// cached like device_block_schedule.
-KeySched device_key_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int *nsplit);
+// residency of `kernel`, with bh0 added to every head index, built,
+// uploaded (stream-ordered on `stream`) and cached like device_block_schedule.
+KeySched device_key_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int *nsplit,
+                             int bh0 = 0, int max_split = -1);
 
 }  // namespace gptc

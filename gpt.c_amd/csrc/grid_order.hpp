@@ -22,6 +22,7 @@
 #include <array>
 #include <climits>
 #include <map>
+#include <mutex>
 #include <utility>
 
 #include "hip_check.hpp"
@@ -58,13 +59,17 @@ GridOrder choose_grid_order(int nblk, int bh_pad, Kernel kernel) {
     // Device properties and the kernel's occupancy, once per device and
     // kernel (this runs on every launch, so no runtime queries after the
     // first).  Keyed on the kernel's address: template variants of a kernel
-    // share one function type but not their register counts.
+    // share one function type but not their register counts.  Both caches
+    // below are shared by every host thread that launches: one lock guards
+    // them.
     struct DeviceInfo {
         int cus_total, per_cu;
     };
+    static std::mutex mu;
     static std::map<std::pair<int, const void *>, DeviceInfo> devices;
     int dev = 0;
     hipCheck(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
     const std::pair<int, const void *> dkey{dev, reinterpret_cast<const void *>(kernel)};
     auto d = devices.find(dkey);
     if (d == devices.end()) {

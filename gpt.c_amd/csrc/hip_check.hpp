@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 
@@ -18,3 +19,9 @@ inline void hip_check(hipError_t err, const char *file, int line) {
 // The one stream every launch, copy and allocation of the library uses
 // (fatal if runtime_init_cuda() has not run).
 hipStream_t gptc_stream_checked();
+
+// The serial of the live alloc_cuda block starting at ptr (0 if it is none):
+// new at each allocation of the block and at each write of the library's
+// tensor data ops into it (gptc_block_written).
+uint64_t gptc_block_serial(const void *ptr);
+void gptc_block_written(const void *ptr);

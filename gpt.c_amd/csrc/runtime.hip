@@ -14,6 +14,11 @@
 // 1 MiB, multiples of 2 MiB above.  When the device runs out of memory the
 // cache is returned to the device and the request retried once.
 //
+// Serials.  Every allocation of a block, and every write the library's
+// tensor data ops make into it, gives the block a new serial: a host-side
+// cache of something derived from a block's contents (the attention mask
+// check) stays valid while the serial is unchanged.
+//
 // Shared blocks.  gptc_retain_cuda() adds an owner to a live block: two
 // tensors can then hold one buffer (the attention layer keeps its output
 // for the backward that way instead of copying it), and the block returns
@@ -34,9 +39,11 @@ bool g_pool_alloc = false;  // device supports stream-ordered allocation
 
 std::mutex g_alloc_mu;
 struct LiveBlock {
-    size_t cls;  // size class
-    int refs;    // owners (1 + retains)
+    size_t cls;       // size class
+    int refs;         // owners (1 + retains)
+    uint64_t serial;  // changes at every allocation of the block and every library write into it
 };
+uint64_t g_serial = 0;
 std::unordered_map<void *, LiveBlock> g_live;  // blocks in use
 std::multimap<size_t, void *> g_cached;     // size class -> free block
 size_t g_cached_bytes = 0;
@@ -133,8 +140,20 @@ extern "C" void *alloc_cuda(const size_t nbytes) {
         }
         hipCheck(err);
     }
-    g_live.emplace(ptr, LiveBlock{cls, 1});
+    g_live.emplace(ptr, LiveBlock{cls, 1, ++g_serial});
     return ptr;
+}
+
+uint64_t gptc_block_serial(const void *ptr) {
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    auto it = g_live.find(const_cast<void *>(ptr));
+    return it == g_live.end() ? 0 : it->second.serial;
+}
+
+void gptc_block_written(const void *ptr) {
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    auto it = g_live.find(const_cast<void *>(ptr));
+    if (it != g_live.end()) it->second.serial = ++g_serial;
 }
 
 extern "C" void gptc_retain_cuda(void *ptr) {

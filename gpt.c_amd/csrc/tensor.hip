@@ -47,6 +47,7 @@ __global__ __launch_bounds__(kThreads) void copy_kernel(float *__restrict__ dst,
 
 void launch_fill(tensor_t *tensor, float value) {
     if (tensor->length == 0) return;
+    gptc_block_written(tensor->t);
     const bool vec = (reinterpret_cast<uintptr_t>(tensor->t) & 15) == 0;
     fill_kernel<<<grid_for(tensor->length / 4 + 1), kThreads, 0, gptc_stream_checked()>>>(tensor->t, tensor->length, value, vec);
     hipCheck(hipGetLastError());
@@ -111,6 +112,7 @@ extern "C" void arange_tensor_data_cuda(tensor_t *tensor, const int start, const
     REQUIRE_ARG(tensor);
     if (!tensor->t) create_tensor_data_cuda(tensor);
     if (tensor->length == 0) return;
+    gptc_block_written(tensor->t);
     arange_kernel<<<grid_for(tensor->length), kThreads, 0, gptc_stream_checked()>>>(tensor->t, tensor->length, start, steps);
     hipCheck(hipGetLastError());
 }
@@ -122,6 +124,7 @@ extern "C" void copy_tensor_data_cuda(tensor_t *dst, const tensor_t *src) {
     CHECK_ERROR(src->t == NULL, "%s(): `src` has no data buffer.", __func__);
     CHECK_ERROR(src->length != dst->length, "tensor copy: source has %d elements, destination %d.", src->length, dst->length);
     if (src->length == 0) return;
+    gptc_block_written(dst->t);
     const bool vec = ((reinterpret_cast<uintptr_t>(dst->t) | reinterpret_cast<uintptr_t>(src->t)) & 15) == 0;
     copy_kernel<<<grid_for(src->length / 4 + 1), kThreads, 0, gptc_stream_checked()>>>(dst->t, src->t, src->length, vec);
     hipCheck(hipGetLastError());

@@ -157,6 +157,7 @@ SIGNATURES = {
     "gptc_set_kernel_events": (None, [ctypes.POINTER(_vp), _ci]),
     "gptc_attention_state_floats": (ctypes.c_longlong, [_ci, _ci, _ci, _ci]),
     "gptc_attention_set_state_limit": (ctypes.c_longlong, [ctypes.c_longlong]),
+    "gptc_attention_set_scratch_limit": (ctypes.c_longlong, [ctypes.c_longlong]),
     "attention_decode_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
     "attention_decode_noalloc_cuda_kernel": (None, [TensorP, TensorP, TensorP, _ci, _ci, TensorP]),
     "gptc_decode_noalloc_scratch_floats": (ctypes.c_longlong, []),

@@ -224,6 +224,9 @@ void zero_grad_adamW_cuda_kernel(tensor_t **gradients, const int n);
  *            token's k and v into row pos.  0 <= pos < L, pos < 8192.
  *   output   (B, 1, C) device: attention output of position pos, equal to row
  *            pos of the forward over tokens 0 .. pos.
+ *   Head size 64 with 16-byte rows: one launch (one workgroup per (b, h))
+ *   for pos < 512; past that a split-key launch over 64-key chunks and a
+ *   merge launch, with a stream-ordered partials buffer.
  */
 void attention_decode_cuda_kernel(
     const tensor_t *qkv,
@@ -239,12 +242,16 @@ void attention_decode_cuda_kernel(
  *   No counterpart in the reference.  For callers that cannot allocate
  *   device memory (code under HIP graph capture, tight serving loops,
  *   harnesses that forbid hipMalloc): the same step, arguments and results
- *   as attention_decode_cuda_kernel, but its partial softmax states go to a
- *   fixed device array (gptc_decode_noalloc_scratch_floats() floats, 4 MiB,
- *   one per GPU, held until the process ends) instead of a stream-ordered
- *   allocation; the call allocates and frees nothing.  A step needing more
- *   partials (B*H*ceil((pos+1)/64)*68 floats) is a fatal error.  Calls that
- *   overlap on one GPU share that array and race.
+ *   as attention_decode_cuda_kernel, but the partial softmax states of its
+ *   split-key steps (head size 64, pos >= 512) go to a fixed device array
+ *   (gptc_decode_noalloc_scratch_floats() floats, 4 MiB, one per GPU, held
+ *   until the process ends) instead of a stream-ordered allocation; the call
+ *   allocates and frees nothing.  A step needing more partials
+ *   (B*H*ceil((pos+1)/64)*68 floats) is a fatal error.  Calls that overlap on
+ *   one GPU share that array and race.  pos is a host argument: a graph
+ *   capture of this call replays that position (and its split count), so
+ *   each position needs its own capture (gptc_gpt2_generate reads the
+ *   position from device memory instead).
  */
 void attention_decode_noalloc_cuda_kernel(
     const tensor_t *qkv,
@@ -318,13 +325,26 @@ long long gptc_attention_state_floats(int B, int T, int C, int n_heads);
  * gptc_attention_set_state_limit(floats): no counterpart in gpt.c.  The
  * largest backward state (in floats) the forward keeps with the probability
  * blocks of P'; a forward whose state would be larger keeps only the
- * log-sum-exp (O(T) per head) when head size 64 runs, and its backward then
- * recomputes P in both gradient kernels (7 contractions instead of 4; slower,
- * same results to the stated tolerance).  Default and floats < 0: the int
+ * log-sum-exp (O(T) per head) when head size 64 runs.  Its backward then
+ * recomputes P in the dK/dV kernel (4 contractions there instead of 3) and
+ * writes dS to a scratch the dQ kernel reads (see the scratch limit below);
+ * same results to the stated tolerance.  Default and floats < 0: the int
  * length of a tensor_t.  0 makes every D = 64 forward keep the LSE-only state.
  * Returns the previous limit.  Applies to forwards that run after the call.
  */
 long long gptc_attention_set_state_limit(long long floats);
+
+/*
+ * gptc_attention_set_scratch_limit(floats): no counterpart in gpt.c.  The
+ * largest dS scratch (in floats) the backward of the LSE-only state
+ * allocates, stream-ordered, for the duration of the call: the packed causal
+ * blocks of as many whole heads as fit (T^2/2 floats per head, roughly),
+ * the heads running in chunks of that many.  If not even one head fits, the
+ * dQ kernel recomputes P and dP from the LSE too (7 contractions in all, no
+ * scratch).  Default, floats < 0 and floats > 2^30: 2^30 floats (4 GiB).
+ * Returns the previous limit.  Applies to backwards that run after the call.
+ */
+long long gptc_attention_set_scratch_limit(long long floats);
 int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
                                   double *max_cu_load, int *used_pairs);
 int gptc_attention_key_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,

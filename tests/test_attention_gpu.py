@@ -6,6 +6,7 @@ and compares with the oracle (the C restatement of gpt.c's OpenBLAS CPU
 path) on the same seeded inputs.  Tolerance, from the BASELINE north star:
 max abs err <= 1e-4 on y, dq, dk, dv and the saved log-sum-exp.
 """
+import contextlib
 import ctypes
 
 import numpy as np
@@ -111,9 +112,48 @@ def test_head_size_128_full_length(rt, oracle):
     compare_with_oracle(rt, oracle, 1, 1024, 1024, 8)
 
 
-def test_head_size_past_128_is_refused():
-    """Head sizes the kernels are not built for end the process with gpt.c's error
-    report before any launch (a host-side check)."""
+@pytest.mark.parametrize("B,T,C,H", [
+    (1, 40, 258, 2),      # D = 129: the smallest generic head size
+    (2, 77, 384, 2),      # D = 192
+    (1, 300, 512, 2),     # D = 256, several key chunks
+    (2, 33, 1024, 2),     # D = 512 (32-key chunks)
+    (1, 21, 1024, 1),     # D = 1024 (8-key chunks), the largest served
+])
+def test_generic_head_sizes_fwd_bwd(rt, oracle, B, T, C, H):
+    """Head sizes past 128 (gpt.c accepts any D with C % H == 0,
+    src/attention.c:23): the generic plain-FMA kernels with the LSE-only
+    state, against the oracle at the same tolerance."""
+    compare_with_oracle(rt, oracle, B, T, C, H)
+
+
+def test_generic_head_size_reference_layout(rt, oracle):
+    """The generic forward with gpt.c's own cache layout (permuted q, k, v
+    in cache[0..2]): the caches hold exactly the permuted inputs."""
+    B, T, C, H = 2, 50, 400, 2  # D = 200
+    x, dy = qkv_inputs(rt, B, T, C, 61, 62)
+    lib = rt.lib
+    xt = rt.from_numpy(x)
+    mask = rt.from_numpy(np.tril(np.ones((T, T), np.float32)))
+    D = C // H
+    caches = (gptc.TensorP * 4)(rt.empty((B, H, T, D)), rt.empty((B, H, T, D)), rt.empty((B, H, T, D)),
+                                rt.empty((B, H, T, T)))
+    yt, dout = rt.empty((B, T, C)), rt.empty((B, T, 3 * C))
+    lib.attention_forward_cuda_kernel(xt, mask, H, caches, yt)
+    y_ref, q, k, v, att = oracle.forward(x, H)
+    check("y", rt.to_numpy(yt), y_ref)
+    for i, ref in enumerate((q, k, v)):
+        assert np.array_equal(rt.to_numpy(caches[i]), ref), f"cache[{i}]"
+    dyt = rt.from_numpy(dy)
+    lib.attention_backward_cuda_kernel(dyt, caches, H, dout)
+    check("dqkv", rt.to_numpy(dout), oracle.backward(dy, H, q, k, v, att))
+    for t in (xt, dyt, mask, yt, dout, *caches):
+        rt.free(t)
+    rt.sync()
+
+
+def test_head_size_past_1024_is_refused():
+    """Head sizes past the generic kernels' 1024 end the process with gpt.c's
+    error report before any launch (a host-side check)."""
     import os
     import subprocess
     import sys
@@ -127,14 +167,14 @@ def test_head_size_past_128_is_refused():
         lib = gptc.load()
         rt = gptc.Runtime(lib)
         rt.init()
-        layer = gptc.AttentionLayer(rt, 516, 2, 4)
+        layer = gptc.AttentionLayer(rt, 2060, 2, 4)
         layer.to(gptc.CUDA)
-        layer.forward(rt.from_numpy(np.zeros((1, 4, 3 * 516), np.float32)))
+        layer.forward(rt.from_numpy(np.zeros((1, 4, 3 * 2060), np.float32)))
         print('survived')
     """)
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 1 and "survived" not in r.stdout, r.stderr
-    assert "Head size 258 is not supported" in r.stderr and "[ERROR]" in r.stderr
+    assert "Head size 1030 is not supported" in r.stderr and "[ERROR]" in r.stderr
 
 
 def test_mask_block_larger_than_T(rt, oracle):
@@ -289,16 +329,38 @@ def lse_only_state(rt):
     rt.lib.gptc_attention_set_state_limit(-1)
 
 
+def ds_floats_per_head(T):
+    """Floats of one head's packed causal dS blocks ([64 queries][32 keys]
+    for key blocks 0 .. 2qt+1 of each 64-query tile qt)."""
+    nqt = (T + 63) // 64
+    return nqt * (nqt + 1) * 64 * 32
+
+
+@contextlib.contextmanager
+def scratch_limit(rt, floats):
+    rt.lib.gptc_attention_set_scratch_limit(floats)
+    try:
+        yield
+    finally:
+        rt.lib.gptc_attention_set_scratch_limit(-1)
+
+
+@pytest.mark.parametrize("scratch", ["whole", "chunks", "none"])
 @pytest.mark.parametrize("B,T,C,H", [(2, 1024, 768, 12), (1, 1000, 768, 12), (1, 200, 128, 2), (2, 100, 256, 4),
-                                     (1, 129, 128, 2), (3, 65, 128, 2), (1, 1, 64, 1)])
-def test_lse_only_state_fwd_bwd(rt, oracle, lse_only_state, B, T, C, H):
-    """The backward that recomputes P from the saved log-sum-exp in both
-    gradient kernels (dk/dv without storing dS; dq recomputing S and dP), used
-    when the probability blocks would exceed the state limit: its state is
-    O(T) per head, and its results meet the same tolerance."""
+                                     (1, 129, 128, 2), (3, 65, 128, 2), (1, 1, 64, 1), (3, 333, 320, 5)])
+def test_lse_only_state_fwd_bwd(rt, oracle, lse_only_state, B, T, C, H, scratch):
+    """The backward of the LSE-only state (its state is O(T) per head), used
+    when the probability blocks would exceed the state limit: the dk/dv
+    kernel recomputes P from the saved log-sum-exp, and dQ comes from dS
+    written to a scratch of every head at once ("whole"), of heads in chunks
+    of at most 5 ("chunks": uneven last chunk where B*H is not a multiple of
+    5), or, with no scratch ("none"), from a dq kernel that recomputes S and
+    dP too.  Each meets the same tolerance."""
     n = rt.lib.gptc_attention_state_floats(B, T, C, H)
     assert n < B * H * T * 8 + B * ((T + 63) // 64) * C + 4 * B * ((T + 127) // 128) * C + 4096
-    compare_with_oracle(rt, oracle, B, T, C, H)
+    limit = {"whole": -1, "chunks": 5 * ds_floats_per_head(T), "none": 0}[scratch]
+    with scratch_limit(rt, limit):
+        compare_with_oracle(rt, oracle, B, T, C, H)
 
 
 def test_long_sequence_past_the_state_cap(rt, oracle):
@@ -380,3 +442,52 @@ def test_device_tensor_ops(rt):
     for x in (t, c, f, z, r):
         rt.free(x)
     rt.sync()
+
+
+MASK_SCRIPT = """
+import sys
+sys.path.insert(0, {pkg!r})
+import numpy as np
+import gptc
+lib = gptc.load()
+rt = gptc.Runtime(lib)
+rt.init()
+B, T, C, H = 1, 96, 128, 2
+x = rt.from_numpy(np.ones((B, T, 3 * C), np.float32))
+n = lib.gptc_attention_state_floats(B, T, C, H)
+caches = (gptc.TensorP * 4)(x, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((n,)))
+m = np.tril(np.ones((T + 4, T + 4), np.float32))
+m[T:, :] = 7.0  # outside the T x T block a call reads: ignored
+mask = rt.from_numpy(m)
+lib.attention_forward_cuda_kernel(x, mask, H, caches, caches[1])
+rt.sync()
+print("causal ok", flush=True)
+{second}
+lib.attention_forward_cuda_kernel(x, mask, H, caches, caches[1])
+rt.sync()
+print("returned", flush=True)
+"""
+
+
+@pytest.mark.parametrize("case", ["edited_entry", "refilled_buffer"])
+def test_non_causal_mask_is_refused(case):
+    """gpt.c applies whatever the mask holds (kernels/src/cpu/Attention.c:139);
+    these kernels apply the causal rule from indices, so a mask that differs
+    from tril on the T x T block is a fatal error before any launch, including
+    a mask the library already checked and then rewrote (the check follows
+    the buffer's allocation serial)."""
+    import os
+    import subprocess
+    import sys
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpt.c_amd")
+    second = {
+        # A fresh buffer whose entry (5, 3) is not 1: a key at or below the diagonal masked out.
+        "edited_entry": "m2 = np.tril(np.ones((T, T), np.float32)); m2[5, 3] = 0.0; mask = rt.from_numpy(m2)",
+        # The checked buffer refilled with ones (future keys visible) through the library.
+        "refilled_buffer": "lib.fill_tensor_data_cuda(mask, 1.0)",
+    }[case]
+    r = subprocess.run([sys.executable, "-c", MASK_SCRIPT.format(pkg=pkg, second=second)], capture_output=True,
+                       text=True, timeout=120)
+    print(r.stdout, r.stderr[-400:])
+    assert "causal ok" in r.stdout, r.stderr
+    assert r.returncode != 0 and "returned" not in r.stdout and "causal mask" in r.stderr, r.stderr

@@ -63,12 +63,16 @@ def decode_all(rt, x, H, L=None):
 @pytest.mark.parametrize("B,T,C,H,L", [
     (1, 1, 64, 1, 1),        # one key: y = v
     (2, 37, 128, 2, 40),     # cache longer than the sequence
-    (1, 300, 768, 12, 300),  # GPT-2 small heads, one key tile of 256 threads and a bit
+    (1, 300, 768, 12, 300),  # GPT-2 small heads: the one-launch kernel (pos + 1 <= 512)
+    (1, 600, 768, 12, 640),  # past 512 keys: the split-key pair from position 512 on
+    (3, 520, 256, 4, 520),   # B = 3, both kernels
     (2, 70, 96, 4, 70),      # D = 24 (plain loads)
     (2, 9, 6, 2, 16),        # D = 3 (gpt.c's tests/test_self_attention.c shape class)
     (1, 64, 100, 25, 64),    # H = 25, D = 4
     (2, 33, 192, 2, 40),     # D = 96
     (1, 40, 256, 2, 48),     # D = 128
+    (1, 30, 600, 2, 32),     # D = 300 (the generic head-size build)
+    (2, 20, 1024, 1, 24),    # D = 1024
 ])
 def test_decode_every_position(rt, oracle, B, T, C, H, L):
     x = rt.normal((B, T, 3 * C), 1337)

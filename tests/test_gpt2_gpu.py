@@ -136,6 +136,7 @@ def test_gpt2_training_steps_match_oracle(rt, oracle, V, block, L, H, C, B, T):
     (2, 77, 96, 4),     # D = 24: the bias is added to the qkv activations instead
     (2, 64, 256, 2),    # D = 128 (the 128-dim kernels), bias added to the activations
     (3, 65, 128, 2),    # two-tile heads with the bias folded into the short-head kernels
+    (2, 50, 384, 2),    # D = 192 (the generic head-size kernels), bias added to the activations
 ])
 def test_self_attention_block_matches_oracle(rt, oracle, B, T, C, H):
     """SelfAttention (self_attention.c:47-83): forward and backward through
@@ -146,16 +147,23 @@ def test_self_attention_block_matches_oracle(rt, oracle, B, T, C, H):
     self_attention_vs_oracle(rt, oracle, B, T, C, H)
 
 
+@pytest.mark.parametrize("scratch", ["whole", "chunks", "none"])
 @pytest.mark.parametrize("B,T,C,H", [(2, 256, 768, 12), (2, 100, 256, 4)])
-def test_self_attention_lse_only_state(rt, oracle, B, T, C, H):
+def test_self_attention_lse_only_state(rt, oracle, B, T, C, H, scratch):
     """The same block with the attention state capped to the log-sum-exp: the
-    bias folded into the recomputing gradient kernels (dq's bias gradient from
-    the recomputing dq kernel's column sums)."""
+    bias folded into the recomputing dk/dv kernel and, with a dS scratch of
+    every head ("whole") or of 5 heads at a time ("chunks"), into the dq
+    kernel that reads it; with no scratch ("none"), dq's bias gradient comes
+    from the recomputing dq kernel's column sums."""
+    nqt = (T + 63) // 64
+    limit = {"whole": -1, "chunks": 5 * nqt * (nqt + 1) * 2048, "none": 0}[scratch]
     rt.lib.gptc_attention_set_state_limit(0)
+    rt.lib.gptc_attention_set_scratch_limit(limit)
     try:
         self_attention_vs_oracle(rt, oracle, B, T, C, H)
     finally:
         rt.lib.gptc_attention_set_state_limit(-1)
+        rt.lib.gptc_attention_set_scratch_limit(-1)
 
 
 def self_attention_vs_oracle(rt, oracle, B, T, C, H):
@@ -191,10 +199,13 @@ def self_attention_vs_oracle(rt, oracle, B, T, C, H):
         check(n, a_, b_)
 
 
-def test_gpt2_c3_real_shape_matches_oracle(rt, oracle):
+@pytest.mark.parametrize("B", [1, 8])
+def test_gpt2_c3_real_shape_matches_oracle(rt, oracle, B):
     """C3's model at its real width and depth (GPT-2 124M: 12 layers, C=768,
-    H=12, V=50257, T=1024, N(0, 0.02) init, zero biases, LayerNorm weight 1)
-    on a B=1 slice: one training step against the oracle's step over the same
+    H=12, V=50257, T=1024, N(0, 0.02) init, zero biases, LayerNorm weight 1),
+    on a B=1 slice and at C3's own batch, B=8 (whose weight-gradient GEMMs
+    reduce over 8192 rows, split four or eight ways into strided-batched
+    slices): one training step against the oracle's step over the same
     batch, at gpt.c's AdamW eps = 1e-8.
 
     Loss, logits and all 148 gradient tensors within 1e-4 x max(1, max|ref|),
@@ -207,7 +218,8 @@ def test_gpt2_c3_real_shape_matches_oracle(rt, oracle):
     of the update on either side (1e-6 lr + 2.4e-7 |p|); outside the tied
     embedding the second group must hold under 20 % of the entries (12 % at
     this init)."""
-    V, block, L, H, C, B, T = 50257, 1024, 12, 12, 768, 1, 1024
+    V, block, L, H, C, T = 50257, 1024, 12, 12, 768, 1024
+    print(f"case C3 real shape B={B} T={T}", flush=True)
     params = init_params(V, block, L, C, seed=2024)
     rng = np.random.default_rng(2025)
     batch = [(rng.integers(0, V, (B, T)), rng.integers(0, V, (B, T)))]

@@ -1,12 +1,13 @@
 """attention_decode_noalloc_cuda_kernel against attention_decode_cuda_kernel.
 
-The allocation-free entry point runs the same split-key decode kernels with
-their partials in a fixed device array instead of a stream-ordered
-allocation, so its output and the cache rows it writes must equal the
-allocating entry point's bit for bit.  Two calls in a row share that array:
-the second, with fewer sequences and keys, must not see the first's
-partials.  A step needing more partials than the array holds is refused on
-the host before any launch.
+The allocation-free entry point runs the same decode kernels; steps past
+512 keys (the split-key pair) keep their partials in a fixed device array
+instead of a stream-ordered allocation, so its output and the cache rows it
+writes must equal the allocating entry point's bit for bit.  Two such calls
+in a row share that array: the second, with fewer sequences and keys, must
+not see the first's partials.  A step of at most 512 keys (one launch, no
+partials) follows them.  A step needing more partials than the array holds
+is refused on the host before any launch.
 """
 import os
 import subprocess
@@ -61,7 +62,8 @@ def reference_row(row, kc, vc, pos, H, D):
 
 
 def test_noalloc_matches_allocating_entry_point_twice(rt):
-    cases = [(4, 12, 64, 1024, 900, 11), (1, 12, 64, 512, 100, 23)]  # second call smaller
+    # Second call smaller; both use the scratch array.  The third needs none.
+    cases = [(4, 12, 64, 1024, 900, 11), (1, 12, 64, 1024, 600, 23), (1, 12, 64, 512, 100, 29)]
     for B, H, D, L, pos, seed in cases:
         (y_a, k_a, v_a), (y_n, k_n, v_n) = decode_both(rt, B, H, D, L, pos, seed)
         assert np.array_equal(y_a, y_n), f"outputs differ at B={B} pos={pos}: {np.abs(y_a - y_n).max():.3e}"
