@@ -758,7 +758,10 @@ def attention_bench(args):
     lse_res, lse_out = None, None
     if not fwd_only and D == 64:
         prev_limit = lib.gptc_attention_set_state_limit(0)
-        for _ in range(args.warmup):
+        # The first step re-points the state; the warm-up then runs long
+        # enough for the clocks to settle on the new kernel mix (the first
+        # K-step pass after 10 steps measured 2 % above the repetitions).
+        for _ in range(max(args.warmup, 40)):
             step()
         rt.sync()
         ms_lse = timed(lambda i: step(), args.steps)
@@ -929,6 +932,10 @@ def attention_bench(args):
     if lse_res is not None:
         lse_res["pct_fp32_mfma_peak"] = round(100.0 * lse_res["tflops"] / peak, 2)
         result["lse_only"] = lse_res
+    # The other workloads, in child processes, when this is the default
+    # (driver) run: C2 with the CPU leg.
+    if args.config == "c2" and not args.no_cpu_baseline and not args.no_other_configs:
+        result["other_configs"] = other_configs(args)
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle over OpenBLAS) ...")
         cb = cpu_baseline(cfg, x, dy, args.cpu_budget_s, gpu_outs)
@@ -940,6 +947,48 @@ def attention_bench(args):
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
+
+
+def other_configs(args):
+    """The benchmark's other workloads, each measured by this script in a
+    child process (no CPU leg there): C5, C1 (cold forward), the C4 decode
+    attention, C4 greedy generation (graph loop) and the C3 training step.
+    They ride in the default run's one JSON line so that every config has a
+    driver-measured figure.  Children start after the parent's GPU work is
+    done and its buffers are freed."""
+    runs = {
+        "c5": ["--config", "c5", "--steps", "30", "--warmup", "5", "--reps", "3", "--no-kernel-pass"],
+        "c1": ["--config", "c1", "--steps", "50", "--warmup", "5", "--reps", "3", "--no-kernel-pass"],
+        "c4_decode_attention": ["--workload", "decode"],
+        "c4_generation": ["--workload", "c4", "--c4-loops", "graph"],
+        "c3_training_step": ["--workload", "gpt2", "--steps", "5", "--warmup", "2"],
+    }
+    keep = ("workload", "metric", "value", "unit", "ms_per_step", "tflops", "pct_fp32_mfma_peak", "pct_hbm_peak",
+            "tokens_per_s", "same_tokens",
+            "us_per_step", "roofline", "lse_only", "kernel_ms", "forward", "kv_cache_graph", "config", "note")
+    out = {}
+    for name, extra in runs.items():
+        cmd = [sys.executable, os.path.abspath(__file__), "--no-cpu-baseline"] + extra
+        log(f"[bench] other config {name}: {' '.join(extra)}")
+        t0 = time.perf_counter()
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=args.other_timeout_s)
+        except subprocess.TimeoutExpired:
+            out[name] = {"error": f"timed out after {args.other_timeout_s} s"}
+            continue
+        lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+        if r.returncode != 0 or not lines:
+            out[name] = {"error": f"exit {r.returncode}", "stderr_tail": r.stderr[-400:]}
+            continue
+        d = json.loads(lines[-1])
+        o = {k: d[k] for k in keep if k in d}
+        if "lse_only" in o:
+            o["lse_only"] = {k: o["lse_only"][k] for k in ("ms_per_step", "tflops", "pct_fp32_mfma_peak")
+                             if k in o["lse_only"]}
+        o["wall_s"] = round(time.perf_counter() - t0, 1)
+        o["command"] = "bench.py --no-cpu-baseline " + " ".join(extra)
+        out[name] = o
+    return out
 
 
 def main():
@@ -963,6 +1012,9 @@ def main():
     ap.add_argument("--no-kernel-pass", action="store_true",
                     help="attention: skip the per-kernel event pass (e.g. under a kernel trace of the headline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="attention C2: skip the other workloads measured in child processes")
+    ap.add_argument("--other-timeout-s", type=float, default=240.0)
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     args = ap.parse_args()
 
