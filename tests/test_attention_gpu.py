@@ -469,7 +469,26 @@ print("returned", flush=True)
 """
 
 
-@pytest.mark.parametrize("case", ["edited_entry", "refilled_buffer"])
+def test_host_mask_is_checked_at_every_call(rt, oracle):
+    """A mask in host memory (the C-ABI accepts one; gpt.c's dispatcher would
+    not pass it) is read directly at every call: the causal buffer runs, and
+    the result matches the oracle."""
+    B, T, C, H = 1, 70, 128, 2
+    x, _ = qkv_inputs(rt, B, T, C, 71, 72)
+    lib = rt.lib
+    xt = rt.from_numpy(x)
+    mask = rt.from_numpy(np.tril(np.ones((T + 2, T + 2), np.float32)), gptc.CPU)
+    n = lib.gptc_attention_state_floats(B, T, C, H)
+    caches = (gptc.TensorP * 4)(xt, rt.empty((B, T, C)), rt.empty((B, H, T)), rt.empty((n,)))
+    lib.attention_forward_cuda_kernel(xt, mask, H, caches, caches[1])
+    y_ref, *_ = oracle.forward(x, H)
+    check("y", rt.to_numpy(caches[1]), y_ref)
+    for t in (mask, *caches):
+        rt.free(t)
+    rt.sync()
+
+
+@pytest.mark.parametrize("case", ["edited_entry", "refilled_buffer", "host_mask"])
 def test_non_causal_mask_is_refused(case):
     """gpt.c applies whatever the mask holds (kernels/src/cpu/Attention.c:139);
     these kernels apply the causal rule from indices, so a mask that differs
@@ -485,6 +504,8 @@ def test_non_causal_mask_is_refused(case):
         "edited_entry": "m2 = np.tril(np.ones((T, T), np.float32)); m2[5, 3] = 0.0; mask = rt.from_numpy(m2)",
         # The checked buffer refilled with ones (future keys visible) through the library.
         "refilled_buffer": "lib.fill_tensor_data_cuda(mask, 1.0)",
+        # A host-memory mask with a visible future key.
+        "host_mask": "m3 = np.tril(np.ones((T, T), np.float32)); m3[2, 9] = 1.0; mask = rt.from_numpy(m3, gptc.CPU)",
     }[case]
     r = subprocess.run([sys.executable, "-c", MASK_SCRIPT.format(pkg=pkg, second=second)], capture_output=True,
                        text=True, timeout=120)
