@@ -714,31 +714,33 @@ attn_fwd_short_kernel(const FwdParams a) {
 // 16-query slab against one 16-key block: slab (j, s) (queries 64j + 16s ..
 // 64j + 16s + 15) sees key blocks 0 .. 4j + s, the last of them its
 // diagonal, so the second block's slabs carry 5 .. 8 units and the first
-// block's 1 .. 4.  Four workgroups per head, each one long and one short
-// slab (9 units), and every slab cut into pieces of at most 3 consecutive
-// key blocks, one piece per wave: no wave carries more than 3 units (96
-// MFMAs).  A wave loads the K and V rows of its piece straight into the
-// registers it uses them from (no staging through LDS, no barrier before
-// the compute), and the pieces of a slab merge their partial softmax states
-// (running max, sums, O) through LDS after the workgroup's one barrier, in
-// a fixed order.
-//   role 0: slabs (1,3) [blocks 0-2 | 3-5 | 6-7] and (0,0) [0]
-//   role 1: slabs (1,2) [0-2 | 3-5 | 6] and (0,1) [0-1]
-//   role 2: slabs (1,1) [0-2 | 3-5] and (0,2) [0-2]
-//   role 3: slabs (1,0) [0-2 | 3-4] and (0,3) [0-1 | 2-3]
+// block's 1 .. 4.  Every slab is cut into pieces of at most 2 consecutive key
+// blocks, one piece per wave: 20 pieces, five workgroups per head, and no
+// wave carries more than 2 units (64 MFMAs), so that a SIMD of a CU holding
+// two workgroups carries at most 4.  A wave loads the K and V rows of its
+// piece straight into the registers it uses them from (no staging through
+// LDS, no barrier before the compute), and the pieces of a slab (all in one
+// workgroup) merge their partial softmax states (running max, sums, O)
+// through LDS after the workgroup's one barrier, in a fixed order, on the
+// wave holding the slab's diagonal block.
+//   role 0: slab (1,3) [blocks 0-1 | 2-3 | 4-5 | 6-7]
+//   role 1: slab (1,2) [0-1 | 2-3 | 4-5 | 6]
+//   role 2: slabs (1,1) [0-1 | 2-3 | 4-5] and (0,0) [0]
+//   role 3: slabs (1,0) [0-1 | 2-3 | 4] and (0,1) [0-1]
+//   role 4: slabs (0,3) [0-1 | 2-3] and (0,2) [0-1 | 2]
 struct SlabState {
     float m_run, l_run;
     f32x4 acc[4];
 };
 
-constexpr int kTwoTileRoles = 4;  // workgroups per head
+constexpr int kTwoTileRoles = 5;  // workgroups per head
 
 // BIAS: the qkv bias is added to the loaded rows (a.qb, a.kb, a.vb set); a
 // separate build, so that the other keeps no registers for it.
 template <bool BIAS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 attn_fwd_twotile_kernel(const FwdParams a) {
-    __shared__ __attribute__((aligned(16))) f32x4 part_lds[2][5][64];  // [partial][acc0..3, {m, l}][lane]
+    __shared__ __attribute__((aligned(16))) f32x4 part_lds[3][5][64];  // [partial][acc0..3, {m, l}][lane]
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -751,10 +753,10 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     const auto q_rows = head_rows(a.q.p + b * a.q.sb + h * a.q.sh, T, a.q.st);
     const auto k_rows = head_rows(a.k.p + b * a.k.sb + h * a.k.sh, T, a.k.st);
     const auto v_rows = head_rows(a.v.p + b * a.v.sb + h * a.v.sh, T, a.v.st);
-    // This wave's slab (block j, slab s); the wave of role 2 with no piece has none.
+    // This wave's slab (block j, slab s).
     const int job = 4 * role + w;  // wave-uniform
-    constexpr int kJobSlab[16][2] = {{1, 3}, {1, 3}, {1, 3}, {0, 0}, {1, 2}, {1, 2}, {1, 2}, {0, 1},
-                                     {1, 1}, {1, 1}, {0, 2}, {-1, 0}, {1, 0}, {1, 0}, {0, 3}, {0, 3}};
+    constexpr int kJobSlab[20][2] = {{1, 3}, {1, 3}, {1, 3}, {1, 3}, {1, 2}, {1, 2}, {1, 2}, {1, 2}, {1, 1}, {1, 1},
+                                     {1, 1}, {0, 0}, {1, 0}, {1, 0}, {1, 0}, {0, 1}, {0, 3}, {0, 3}, {0, 2}, {0, 2}};
     const int sj = kJobSlab[job][0], ss = kJobSlab[job][1];
     // The qkv bias: key rows past T then hold the bias; they are masked for
     // every query < T, and rows of queries past T are not written.
@@ -762,7 +764,7 @@ attn_fwd_twotile_kernel(const FwdParams a) {
     // The Q rows and bias are requested here and added in piece(), after
     // the K and V requests, so that no wait comes before those are issued.
     f32x4 qr[4], qb4[4];
-    if (sj >= 0) {
+    {
         const int q = sj * kF16Rows + 16 * ss + i16;
 #pragma unroll
         for (int c = 0; c < 4; ++c) qr[c] = buffer_load4(q_rows, static_cast<uint32_t>(q) * a.q.st + 16 * c + 4 * g);
@@ -847,35 +849,40 @@ attn_fwd_twotile_kernel(const FwdParams a) {
         st.m_run = m;
     };
 
-    // Compute phase: at most 3 units per wave.
+    // Compute phase: at most 2 units per wave.
     using F = std::false_type;
     using D = std::true_type;
     switch (job) {
-        case 0: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
-        case 1: piece(IntC<3>{}, IntC<3>{}, F{}); put_partial(1); break;
-        case 2: piece(IntC<6>{}, IntC<2>{}, D{}); break;
-        case 3: piece(IntC<0>{}, IntC<1>{}, D{}); finish(); break;
-        case 4: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
-        case 5: piece(IntC<3>{}, IntC<3>{}, F{}); put_partial(1); break;
-        case 6: piece(IntC<6>{}, IntC<1>{}, D{}); break;
-        case 7: piece(IntC<0>{}, IntC<2>{}, D{}); finish(); break;
-        case 8: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
-        case 9: piece(IntC<3>{}, IntC<3>{}, D{}); break;
-        case 10: piece(IntC<0>{}, IntC<3>{}, D{}); finish(); break;
-        case 11: break;
-        case 12: piece(IntC<0>{}, IntC<3>{}, F{}); put_partial(0); break;
-        case 13: piece(IntC<3>{}, IntC<2>{}, D{}); break;
-        case 14: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(1); break;
-        default: piece(IntC<2>{}, IntC<2>{}, D{}); break;
+        case 0: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(0); break;
+        case 1: piece(IntC<2>{}, IntC<2>{}, F{}); put_partial(1); break;
+        case 2: piece(IntC<4>{}, IntC<2>{}, F{}); put_partial(2); break;
+        case 3: piece(IntC<6>{}, IntC<2>{}, D{}); break;
+        case 4: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(0); break;
+        case 5: piece(IntC<2>{}, IntC<2>{}, F{}); put_partial(1); break;
+        case 6: piece(IntC<4>{}, IntC<2>{}, F{}); put_partial(2); break;
+        case 7: piece(IntC<6>{}, IntC<1>{}, D{}); break;
+        case 8: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(0); break;
+        case 9: piece(IntC<2>{}, IntC<2>{}, F{}); put_partial(1); break;
+        case 10: piece(IntC<4>{}, IntC<2>{}, D{}); break;
+        case 11: piece(IntC<0>{}, IntC<1>{}, D{}); finish(); break;
+        case 12: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(0); break;
+        case 13: piece(IntC<2>{}, IntC<2>{}, F{}); put_partial(1); break;
+        case 14: piece(IntC<4>{}, IntC<1>{}, D{}); break;
+        case 15: piece(IntC<0>{}, IntC<2>{}, D{}); finish(); break;
+        case 16: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(0); break;
+        case 17: piece(IntC<2>{}, IntC<2>{}, D{}); break;
+        case 18: piece(IntC<0>{}, IntC<2>{}, F{}); put_partial(1); break;
+        default: piece(IntC<2>{}, IntC<1>{}, D{}); break;
     }
     __syncthreads();
     // Merge phase: the diagonal piece of a split slab takes in the others.
     switch (job) {
-        case 2:
-        case 6: merge(0); merge(1); finish(); break;
-        case 9:
-        case 13: merge(0); finish(); break;
-        case 15: merge(1); finish(); break;
+        case 3:
+        case 7: merge(0); merge(1); merge(2); finish(); break;
+        case 10:
+        case 14: merge(0); merge(1); finish(); break;
+        case 17: merge(0); finish(); break;
+        case 19: merge(1); finish(); break;
         default: break;
     }
 }
