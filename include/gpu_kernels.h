@@ -67,8 +67,10 @@ void copy_tensor_data_cuda(tensor_t *dst, const tensor_t *src);
  *            re-pointed to a 1-D buffer holding the output copy, the
  *            log-sum-exp and the backward state (about half the size of
  *            the B*H*T*T probability matrix gpt.c keeps there).
- *   Supported head sizes: D <= 128 (D = C / n_heads).  The state must fit
- *   the int length of a tensor_t (checked, fatal otherwise).
+ *   Supported head sizes: 1 <= D <= 1024 (D = C / n_heads; fatal before
+ *   any launch otherwise).  D <= 128 runs the MFMA kernels, 128 < D <= 1024
+ *   plain-FMA kernels that keep the LSE-only state.  The state must fit the
+ *   int length of a tensor_t (checked, fatal otherwise).
  *
  * attention_backward_cuda_kernel(global_grad, cache, n_heads, dout)
  *   global_grad (B, T, C) upstream gradient (may be clobbered by the caller
