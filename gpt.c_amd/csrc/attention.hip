@@ -186,26 +186,33 @@ void check_causal_mask(const tensor_t *mask, int T) {
         std::lock_guard<std::mutex> lk(g_mask_mu);
         if (g_causal_masks.count(key)) return;
     }
-    std::vector<float> m(static_cast<size_t>(T) * T);
-    if (on_device) {
-        hipStream_t s = gptc_stream_checked();
-        hipCheck(hipMemcpy2DAsync(m.data(), static_cast<size_t>(T) * sizeof(float), mask->t,
-                                  static_cast<size_t>(stride) * sizeof(float), static_cast<size_t>(T) * sizeof(float),
-                                  T, hipMemcpyDeviceToHost, s));
-        hipCheck(hipStreamSynchronize(s));
-    } else {
-        for (int i = 0; i < T; i++)
-            std::copy(mask->t + static_cast<size_t>(i) * stride, mask->t + static_cast<size_t>(i) * stride + T,
-                      m.begin() + static_cast<size_t>(i) * T);
-    }
-    for (int i = 0; i < T; i++)
-        for (int j = 0; j < T; j++) {
-            const bool keep = m[static_cast<size_t>(i) * T + j] == 1.0f;
-            CHECK_ERROR(keep != (j <= i),
-                        "The GPU attention kernels apply the causal mask (mask[i][j] == 1 exactly for j <= i); this "
-                        "mask differs at (%d, %d) (value %g).",
-                        i, j, (double)m[static_cast<size_t>(i) * T + j]);
+    // Rows in chunks, so that the host copy stays small at any T.
+    const int chunk = std::max(1, std::min(T, (1 << 22) / T));
+    std::vector<float> m(static_cast<size_t>(chunk) * T);
+    for (int i0 = 0; i0 < T; i0 += chunk) {
+        const int rows = std::min(chunk, T - i0);
+        const float *src = mask->t + static_cast<size_t>(i0) * stride;
+        if (on_device) {
+            hipStream_t s = gptc_stream_checked();
+            hipCheck(hipMemcpy2DAsync(m.data(), static_cast<size_t>(T) * sizeof(float), src,
+                                      static_cast<size_t>(stride) * sizeof(float),
+                                      static_cast<size_t>(T) * sizeof(float), rows, hipMemcpyDeviceToHost, s));
+            hipCheck(hipStreamSynchronize(s));
+        } else {
+            for (int r = 0; r < rows; r++)
+                std::copy(src + static_cast<size_t>(r) * stride, src + static_cast<size_t>(r) * stride + T,
+                          m.begin() + static_cast<size_t>(r) * T);
         }
+        for (int r = 0; r < rows; r++)
+            for (int j = 0; j < T; j++) {
+                const int i = i0 + r;
+                const float v = m[static_cast<size_t>(r) * T + j];
+                CHECK_ERROR((v == 1.0f) != (j <= i),
+                            "The GPU attention kernels apply the causal mask (mask[i][j] == 1 exactly for j <= i); "
+                            "this mask differs at (%d, %d) (value %g).",
+                            i, j, (double)v);
+            }
+    }
     if (serial != 0) {
         std::lock_guard<std::mutex> lk(g_mask_mu);
         g_causal_masks.insert(key);
