@@ -43,9 +43,9 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Keys (or queries) per staged chunk for head size D (a power of two, 8 to
-// 64): the two tiles of KC x (D + 1) and KC x D floats and the waves' rows
-// stay within 150 KB of LDS.
+// Keys (or queries) per staged chunk for head size D: the largest of 64, 32,
+// 16 and 8 with which the two tiles of KC x (D + 1) and KC x D floats, the
+// waves' rows and weights (and 2 KB of static LDS) stay within 150 KB.
 __host__ __device__ inline int generic_chunk(int D) {
     const int kc = (150 * 1024 / 4 - 2 * kGenWaves * D - kGenWaves * 64 - 512) / (2 * D + 1);
     return kc >= 64 ? 64 : (kc >= 32 ? 32 : (kc >= 16 ? 16 : 8));
@@ -207,8 +207,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_generic_kernel(const BwdParam
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_generic_kernel(const BwdParams a) {
     extern __shared__ float lds[];
     const int D = a.D, T = a.T, kc = generic_chunk(D);
-    // A tile: Q rows (stride D + 1), B tile: dO rows; per wave its K and V row;
-    // weights: P (first 32 of a wave's 64) ... stored as two arrays below.
+    // A tile: Q rows (stride D + 1), B tile: dO rows; per wave its K and V
+    // rows; p_s: each wave's P of the chunk's queries (dS in ds_s).
     float *q_s = lds, *g_s = q_s + kc * (D + 1), *k_s = g_s + kc * D, *v_s = k_s + kGenWaves * D;
     float *p_s = k_s + 2 * kGenWaves * D;  // [w][64]: P of the chunk's queries
     __shared__ float ds_s[kGenWaves][64];    // dS of the chunk's queries
