@@ -508,14 +508,21 @@ attn_fwd16_kernel(const FwdParams a) {
         // the SIMDs otherwise issue from the oldest waves first, so the first
         // workgroup of a CU runs ahead and the last runs alone at the end;
         // workgroups that fall behind now win the MFMA pipe and catch up
-        // (C2 forward 133.8 -> 131.0 us, C5 139.8 -> 137.0 us).
+        // (C2 forward 133.8 -> 131.0 us, C5 139.8 -> 137.0 us).  The levels
+        // change when 40 %, 20 % and 7 % of the list remain: within a level
+        // the oldest workgroup still runs first, so the last levels are the
+        // short ones (the three workgroups of a CU then end closer together;
+        // C2 127.0 against 128.2 us with quarters).
         if (!DEEP) {
-            switch ((4 * (total_steps - done_steps)) / (total_steps + 1)) {  // wave-uniform
-                case 0: __builtin_amdgcn_s_setprio(0); break;
-                case 1: __builtin_amdgcn_s_setprio(1); break;
-                case 2: __builtin_amdgcn_s_setprio(2); break;
-                default: __builtin_amdgcn_s_setprio(3); break;
-            }
+            const int rem100 = 100 * (total_steps - done_steps);  // wave-uniform
+            if (rem100 > 40 * total_steps)
+                __builtin_amdgcn_s_setprio(3);
+            else if (rem100 > 20 * total_steps)
+                __builtin_amdgcn_s_setprio(2);
+            else if (rem100 > 7 * total_steps)
+                __builtin_amdgcn_s_setprio(1);
+            else
+                __builtin_amdgcn_s_setprio(0);
             ++done_steps;
         }
         // The bias of this step's head; the previous step's readers of
