@@ -385,13 +385,31 @@ attn_fwd16_kernel(const FwdParams a) {
     // The qkv bias of the current step's head (q | k | v, 64 floats each).
     __shared__ __attribute__((aligned(16))) float bias_lds[3 * kDPad];
 
+    // The pool's item for the prefetch cursor's next block (see below).
+    __shared__ int pool_lds;
+
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, g = lane >> 4, i16 = lane & 15;
+    // The pool (block_sched.hpp): blocks that no list holds, taken one at a
+    // time by the workgroups whose lists are done.
+    const bool use_pool = !DEEP && !PERM && a.sched.pool_n > 0;
+    // Thread 0 counts the workgroup done; the last one resets the counters.
+    auto pool_done = [&]() {
+        if (use_pool && tid == 0) {
+            const int d = __hip_atomic_fetch_add(a.sched.counters + 64, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d == static_cast<int>(gridDim.x) - 1) {
+                __hip_atomic_store(a.sched.counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(a.sched.counters + 64, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    };
     const int it_end = a.sched.wg_start[blockIdx.x + 1];
     int it = a.sched.wg_start[blockIdx.x];
-    const int it_first = it;  // a register: re-reading the table would wait for every load in flight
-    if (it >= it_end) return;
+    if (it >= it_end) {
+        pool_done();
+        return;
+    }
     const int T = a.T, nqt = a.nqt;
 
     // Cooperative tile load: thread covers rows (tid>>4) + 16i, dims 4*(tid&15).
@@ -423,18 +441,46 @@ attn_fwd16_kernel(const FwdParams a) {
         if (bias_lane) bd = *reinterpret_cast<const f32x4 *>(bias_src + hh * kDPad + bias_dim);
     };
     // The step after (sit, skt) of block sj: the next tile of the block, or
-    // tile 0 of the next block of the list.  False at the end of the list.
+    // tile 0 of the next block of the list, or of the pool's block pool_item
+    // once the list is done (sit == it_end).  False at the end.
+    int pool_item = -1;  // uniform: the pool block published for the prefetch cursor
     auto advance = [&](int &sit, int &skt, int &sbh, int &sj) {
         if (skt < sj) {
             ++skt;
             return true;
         }
-        if (++sit >= it_end) return false;
-        const int item = load_uniform_int(a.sched.items + sit);
-        sbh = sched_bh(item);
-        sj = sched_j(item);
+        if (sit + 1 < it_end) {
+            ++sit;
+            const int item = load_uniform_int(uniform(a.sched.items + sit));
+            sbh = sched_bh(item);
+            sj = sched_j(item);
+            skt = 0;
+            return true;
+        }
+        sit = it_end;
+        if (pool_item < 0) return false;
+        sbh = sched_bh(pool_item);
+        sj = sched_j(pool_item);
         skt = 0;
         return true;
+    };
+    // The pool index for the block after the prefetch cursor's is taken one
+    // step ahead, when that cursor reaches the last tile of the last block it
+    // has: thread 0's atomic (`grab`), published through pool_lds before the
+    // next step's first barrier and read between its two barriers, so the
+    // cursor has it when it moves on after the second.
+    // Wave 0 takes the index as a whole so that no branch here is divergent
+    // (a lane-0 branch made the compiler keep the cursors in vector
+    // registers, with spills): lane 0 adds 1 to counters[0], lanes 1..63 add
+    // 0 to counters[1..63], so the 64 device-scope atomics fall in one cache
+    // line (all 64 on counters[0] cost about 2 us per forward at C2).
+    bool grab = false;  // uniform
+    int grab_idx = 0;   // wave 0's (lane 0's result)
+    auto take_pool_index = [&](int sit, int skt, int sj) {
+        grab = use_pool && skt == sj && sit + 1 >= it_end;
+        if (grab && w == 0)
+            grab_idx = __hip_atomic_fetch_add(a.sched.counters + lane, lane == 0 ? 1 : 0, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
     };
 
     // Steps (key tiles) of this workgroup's list, for the wave priority below.
@@ -443,6 +489,7 @@ attn_fwd16_kernel(const FwdParams a) {
     int done_steps = 0;
     // Current step (it, kt) of block jq of head bh.
     int kt = 0, bh = sched_bh(a.sched.items[it]), jq = sched_j(a.sched.items[it]);
+    bool first_block = true;
     int b = bh / a.H, h = bh - b * a.H;
     const float c2 = a.scale_log2;
     f32x4 qr[4];  // Q[my_q][16c + 4g + e] in qr[c][e]: the B operand of step 4c + e
@@ -454,10 +501,12 @@ attn_fwd16_kernel(const FwdParams a) {
     };
     load_q();
     load_tile(bh, 0, kpre, vpre, bpre);
-    // Prefetch cursor: the step whose tile sits in kpre2 (DEEP) or is loaded next.
+    // Prefetch cursor: the step whose tile sits in kpre2 (DEEP) or is loaded
+    // next; without DEEP the current step follows it.
     int pit = it, pkt = 0, pbh = bh, pj = jq;
     bool pre_ok = advance(pit, pkt, pbh, pj);
     if (DEEP && pre_ok) load_tile(pbh, pkt, kpre2, vpre2, bpre2);
+    if (pre_ok) take_pool_index(pit, pkt, pj);
 
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4 acc[4];  // O^T: acc[db][r] = O[my_q][16g + 4r + db] before the 1/l scaling
@@ -492,7 +541,8 @@ attn_fwd16_kernel(const FwdParams a) {
         if (kt == 0) {
             // A new block: fresh statistics (its Q rows are loaded already
             // for the first block, here for the others).
-            if (it != it_first) load_q();
+            if (!first_block) load_q();
+            first_block = false;
             if (PERM && my_q < T) {
                 float *dst = a.qp + (static_cast<uint32_t>(bh) * T + my_q) * kDPad + 4 * g;
 #pragma unroll
@@ -526,9 +576,19 @@ attn_fwd16_kernel(const FwdParams a) {
             ++done_steps;
         }
         // The bias of this step's head; the previous step's readers of
-        // bias_lds are past its second barrier.
+        // bias_lds are past its second barrier.  Likewise the pool index
+        // taken during the previous step (its readers too).
         if (bias_lane) *reinterpret_cast<f32x4 *>(&bias_lds[4 * tid]) = bpre;
+        if (grab && w == 0) {
+            const int r = __builtin_amdgcn_readfirstlane(grab_idx);
+            if (lane == 0)
+                pool_lds = r < a.sched.pool_n
+                               ? ((a.sched.pool_bh0 + r % a.sched.pool_bh) << kSchedJBits) |
+                                     (a.sched.pool_j0 - 1 - r / a.sched.pool_bh)
+                               : -1;
+        }
         __syncthreads();
+        if (grab) pool_item = __builtin_amdgcn_readfirstlane(pool_lds);
         if (biased) {
             // Rows past T read as zeros and then hold the bias: they only
             // occur in a block's diagonal tile, beyond the diagonal of every
@@ -562,9 +622,13 @@ attn_fwd16_kernel(const FwdParams a) {
         // Refill the prefetch registers with the next step's tile.  DEEP: it
         // is in flight already (kpre2); it moves up after this step's tile,
         // so that this tile's compute does not wait for its loads.
+        const bool has_next = pre_ok;
+        const int n_kt = pkt, n_bh = pbh, n_j = pj;  // without DEEP: the next step
         if (!DEEP && pre_ok) {
             load_tile(pbh, pkt, kpre, vpre, bpre);
             pre_ok = advance(pit, pkt, pbh, pj);
+            grab = false;
+            if (pre_ok) take_pool_index(pit, pkt, pj);
         }
         if (biased && kt == 0) {
 #pragma unroll
@@ -605,10 +669,18 @@ attn_fwd16_kernel(const FwdParams a) {
             pre_ok = advance(pit, pkt, pbh, pj);
             if (pre_ok) load_tile(pbh, pkt, kpre2, vpre2, bpre2);
         }
-        if (!advance(it, kt, bh, jq)) break;
+        if (DEEP) {
+            if (!advance(it, kt, bh, jq)) break;
+        } else {
+            if (!has_next) break;
+            kt = n_kt;
+            bh = n_bh;
+            jq = n_j;
+        }
         b = bh / a.H;
         h = bh - b * a.H;
     }
+    pool_done();
 }
 
 // ---- Short heads (T <= 128, D == 64, compact layout) ----
@@ -927,7 +999,9 @@ void launch_attn_fwd(const FwdParams &p_in, hipStream_t stream, const hipEvent_t
                                 : (perm ? reinterpret_cast<const void *>(attn_fwd16_kernel<true, false>)
                                         : reinterpret_cast<const void *>(attn_fwd16_kernel<false, false>));
         int num_wg = 0;
-        p.sched = device_block_schedule(p.B * p.H, p.nqt, kern, stream, &num_wg);
+        // The pool serves the compact layout's kernel only (the DEEP and PERM
+        // variants keep whole lists).
+        p.sched = device_block_schedule(p.B * p.H, p.nqt, kern, stream, &num_wg, 0, !deep && !perm);
         const dim3 grid(num_wg), block(256);
         if (ev) hipCheck(hipEventRecord(ev[0], stream));
         if (deep && perm)

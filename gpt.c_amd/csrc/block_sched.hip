@@ -34,9 +34,10 @@ double max_cu_load(const SchedTable &t, int cus) {
     return *std::max_element(load.begin(), load.end());
 }
 
-// Workgroup = blocks j and nqt-1-j of one head; heads fastest, so the pairs
-// of a head land on one XCD (blockIdx % 8 == bh % 8).
-SchedTable pairs_schedule(int BH, int nqt) {
+// Workgroup = blocks j and nqt-1-j of one head, less the blocks j < j0 (the
+// pool's); heads fastest, so the pairs of a head land on one XCD
+// (blockIdx % 8 == bh % 8).
+SchedTable pairs_schedule(int BH, int nqt, int j0) {
     SchedTable t;
     const int bh_pad = (BH + kSchedXcds - 1) / kSchedXcds * kSchedXcds, nbh_x = bh_pad / kSchedXcds;
     const int npair = (nqt + 1) / 2;
@@ -46,8 +47,8 @@ SchedTable pairs_schedule(int BH, int nqt) {
         const int x = w % kSchedXcds, i = w / kSchedXcds;
         const int pair = i / nbh_x, bh = x + kSchedXcds * (i - pair * nbh_x);
         if (bh < BH) {
-            t.items.push_back(pack(bh, pair));
-            if (nqt - 1 - pair != pair) t.items.push_back(pack(bh, nqt - 1 - pair));
+            if (pair >= j0) t.items.push_back(pack(bh, pair));
+            if (nqt - 1 - pair != pair && nqt - 1 - pair >= j0) t.items.push_back(pack(bh, nqt - 1 - pair));
         }
         t.wg_start.push_back(static_cast<int>(t.items.size()));
     }
@@ -55,19 +56,19 @@ SchedTable pairs_schedule(int BH, int nqt) {
     return t;
 }
 
-SchedTable lpt_schedule(int BH, int nqt, int per_cu, int cus) {
+SchedTable lpt_schedule(int BH, int nqt, int per_cu, int cus, int j0) {
     struct Item {
         double cost;
         int bh, j;
     };
     double per_head = 0.0;
-    for (int j = 0; j < nqt; ++j) per_head += block_cost(j);
+    for (int j = j0; j < nqt; ++j) per_head += block_cost(j);
     const double target = per_head * BH / kSchedXcds;
     // Heads dealt to XCDs in contiguous ranges of equal work (block granularity).
     std::vector<std::vector<Item>> xitems(kSchedXcds);
     double acc = 0.0;
     for (int bh = 0; bh < BH; ++bh)
-        for (int j = 0; j < nqt; ++j) {
+        for (int j = j0; j < nqt; ++j) {
             const double c = block_cost(j);
             const int x = std::min(static_cast<int>((acc + 0.5 * c) / target), kSchedXcds - 1);
             xitems[x].push_back({c, bh, j});
@@ -208,7 +209,8 @@ struct DeviceTable {
     int num_wg = 0;
     int *wg_start = nullptr;
     int *items = nullptr;
-    SchedTable host;  // kept: the source of the stream-ordered upload
+    int *counters = nullptr;  // the pool's two counters (nullptr: no pool)
+    SchedTable host;          // kept: the source of the stream-ordered upload
 };
 
 struct DeviceKeyTable {
@@ -266,34 +268,54 @@ KeyTable build_key_schedule(int BH, int nqt, int per_cu, int cus, int max_split)
     return std::move(cand.front());
 }
 
-SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus) {
-    CHECK_ERROR(BH < 0 || nqt < 1 || nqt > (1 << kSchedJBits) || per_cu < 1 || cus < 1 ||
-                    static_cast<long long>(BH) >= (1LL << (31 - kSchedJBits)),
-                "block schedule: unsupported shape (heads %d, blocks %d, per CU %d, CUs %d).", BH, nqt, per_cu, cus);
-    SchedTable best = pairs_schedule(BH, nqt);
+namespace {
+
+SchedTable build_with(int BH, int nqt, int per_cu, int cus, int j0) {
+    SchedTable best = pairs_schedule(BH, nqt, j0);
     best.max_cu_load = max_cu_load(best, cus);
-    SchedTable lpt = lpt_schedule(BH, nqt, per_cu, cus);
+    SchedTable lpt = lpt_schedule(BH, nqt, per_cu, cus, j0);
     lpt.max_cu_load = max_cu_load(lpt, cus);
     // Pairs on ties: equal cost per workgroup also balances the workgroups of a CU.
     if (lpt.max_cu_load < best.max_cu_load - 1e-9) best = std::move(lpt);
+    best.pool_j0 = j0;
     return best;
 }
 
-BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int bh0) {
+}  // namespace
+
+SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus, bool pool) {
+    CHECK_ERROR(BH < 0 || nqt < 1 || nqt > (1 << kSchedJBits) || per_cu < 1 || cus < 1 ||
+                    static_cast<long long>(BH) >= (1LL << (31 - kSchedJBits)),
+                "block schedule: unsupported shape (heads %d, blocks %d, per CU %d, CUs %d).", BH, nqt, per_cu, cus);
+    if (pool && nqt > 2 * kPoolJ0) {
+        SchedTable t = build_with(BH, nqt, per_cu, cus, kPoolJ0);
+        bool every_list_used = true;
+        for (int w = 0; w < t.num_wg; ++w) every_list_used = every_list_used && t.wg_start[w + 1] > t.wg_start[w];
+        if (every_list_used) return t;
+    }
+    return build_with(BH, nqt, per_cu, cus, 0);
+}
+
+BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int bh0,
+                                 bool pool) {
     int dev = 0;
     hipCheck(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_mu);
     const auto occ = occupancy_locked(dev, kernel);
     const int per_cu = occ.first, cus = occ.second;
-    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus, bh0);
+    const auto key = std::make_tuple(dev, BH, nqt, per_cu * 1024 + cus, bh0 * 2 + (pool ? 1 : 0));
     auto it = g_tables.find(key);
     if (it == g_tables.end()) {
         check_not_capturing(stream, "work list");
         CHECK_ERROR(static_cast<long long>(bh0) + BH >= (1LL << (31 - kSchedJBits)),
                     "block schedule: head index %d beyond the work-list format.", bh0 + BH);
         DeviceTable d;
-        d.host = build_block_schedule(BH, nqt, per_cu, cus);
+        d.host = build_block_schedule(BH, nqt, per_cu, cus, pool);
         for (int &item : d.host.items) item += bh0 << kSchedJBits;
+        if (d.host.pool_j0 > 0) {
+            hipCheck(hipMalloc(&d.counters, 128 * sizeof(int)));
+            hipCheck(hipMemsetAsync(d.counters, 0, 128 * sizeof(int), stream));
+        }
         d.num_wg = d.host.num_wg;
         const size_t nw = d.host.wg_start.size() * sizeof(int), ni = std::max<size_t>(1, d.host.items.size()) * sizeof(int);
         hipCheck(hipMalloc(&d.wg_start, nw));
@@ -305,7 +327,9 @@ BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_
         it = g_tables.emplace(key, std::move(d)).first;
     }
     *num_wg = it->second.num_wg;
-    return BlockSched{it->second.wg_start, it->second.items};
+    const DeviceTable &t = it->second;
+    const int j0 = t.host.pool_j0;
+    return BlockSched{t.wg_start, t.items, j0 * BH, j0, BH, bh0, t.counters};
 }
 
 KeySched device_key_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int *nsplit,
@@ -351,6 +375,19 @@ extern "C" int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cu
     std::copy(t.items.begin(), t.items.end(), items);
     if (max_cu_load) *max_cu_load = t.max_cu_load;
     if (used_pairs) *used_pairs = t.pairs ? 1 : 0;
+    return t.num_wg;
+}
+
+// The same with the pool (the table device_block_schedule builds with pool
+// true): fills the lists like gptc_attention_block_schedule and returns
+// num_wg; *pool_j0 receives the pool's blocks per head (0: no pool).
+extern "C" int gptc_attention_block_schedule_pool(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items,
+                                                  int cap, int *pool_j0) {
+    const gptc::SchedTable t = gptc::build_block_schedule(BH, nqt, per_cu, cus, true);
+    if (static_cast<int>(t.items.size()) > cap || t.num_wg + 1 > cap) return -1;
+    std::copy(t.wg_start.begin(), t.wg_start.end(), wg_start);
+    std::copy(t.items.begin(), t.items.end(), items);
+    if (pool_j0) *pool_j0 = t.pool_j0;
     return t.num_wg;
 }
 

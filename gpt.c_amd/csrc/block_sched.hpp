@@ -22,6 +22,17 @@
 // Placement uses the dispatch order measured on the MI355X: workgroup
 // blockIdx runs on XCD blockIdx % 8, and the i-th workgroup of an XCD
 // (i = blockIdx / 8) on CU i % cus in dispatch round i / cus.
+//
+// A table may also hold a pool: the blocks j < pool_j0 of every head are
+// then left out of the lists, and a workgroup whose list is done takes them
+// one at a time, largest first, from a counter in device memory (pool item
+// r = block pool_j0 - 1 - r / BH of head r % BH).  The workgroups of a CU do
+// not progress at the same rate (the SIMDs issue from the oldest waves
+// first) and neither do the CUs, so static lists of equal cost do not end
+// together; the pool lets the first ones to finish take the remainder.
+// Every workgroup takes exactly one index at or past the pool's end, after
+// which it stops; the last workgroup to finish resets the counters for the
+// next launch.  Launches that share a table must not overlap.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -37,6 +48,10 @@ constexpr int kSchedXcds = 8;
 struct BlockSched {
     const int *wg_start;  // num_wg + 1 offsets into items
     const int *items;     // (bh << kSchedJBits) | j
+    int pool_n;           // pool items (0: no pool)
+    int pool_j0, pool_bh, pool_bh0;  // pool item r: head pool_bh0 + r % pool_bh, block pool_j0 - 1 - r / pool_bh
+    int *counters;        // 128 ints: [0] next pool index, [64] workgroups done, [1..63] unused
+                          // (zero between launches; see the forward's pool protocol)
 };
 
 __device__ __forceinline__ int sched_bh(int item) { return item >> kSchedJBits; }
@@ -48,11 +63,15 @@ struct SchedTable {
     std::vector<int> wg_start, items;
     double max_cu_load = 0.0;  // largest per-CU sum of block costs (tiles)
     bool pairs = false;        // which construction won
+    int pool_j0 = 0;           // blocks j < pool_j0 of every head form the pool (0: none)
 };
 
 // Builds the table for BH heads of nqt blocks, for a kernel that keeps
-// per_cu workgroups resident per CU on an XCD of cus CUs.
-SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus);
+// per_cu workgroups resident per CU on an XCD of cus CUs.  pool: leave the
+// smallest blocks to a pool (kPoolJ0 of them per head) where every list
+// keeps at least one block; otherwise, or with pool false, there is none.
+SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus, bool pool = false);
+constexpr int kPoolJ0 = 3;  // pool blocks per head: j = 0, 1, 2 (6 of a head's tiles)
 
 // The device copy of build_block_schedule(BH, nqt, per_cu of `kernel`) for
 // the current device, with bh0 added to every head index (the heads
@@ -60,7 +79,8 @@ SchedTable build_block_schedule(int BH, int nqt, int per_cu, int cus);
 // `stream`) on first use and cached for the life of the process.  The first
 // use of a shape must not happen while `stream` is being captured into a
 // graph (it allocates and copies from host memory): that is a fatal error.
-BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int bh0 = 0);
+BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_t stream, int *num_wg, int bh0 = 0,
+                                 bool pool = false);
 
 // ---- Work lists of the D = 64 dk/dv kernel ----
 //

@@ -170,6 +170,8 @@ SIGNATURES = {
     "gptc_attention_backward_qkv_bias": (None, [TensorP, ctypes.POINTER(TensorP), TensorP, _ci, TensorP, TensorP]),
     "gptc_attention_block_schedule": (_ci, [_ci, _ci, _ci, _ci, ctypes.POINTER(_ci), ctypes.POINTER(_ci), _ci,
                                              ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_ci)]),
+    "gptc_attention_block_schedule_pool": (_ci, [_ci, _ci, _ci, _ci, ctypes.POINTER(_ci), ctypes.POINTER(_ci), _ci,
+                                                  ctypes.POINTER(_ci)]),
     "gptc_attention_key_schedule": (_ci, [_ci, _ci, _ci, _ci, ctypes.POINTER(_ci), ctypes.POINTER(_ci), _ci,
                                            ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_ci)]),
     "saxpy_cuda": (None, [_ci, _cf, TensorP, _ci, _ci, TensorP, _ci, _ci]),

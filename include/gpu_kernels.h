@@ -290,6 +290,13 @@ long long gptc_decode_noalloc_scratch_floats(void);
  *   max_cu_load receives the largest per-CU sum of block costs (j + 1.5
  *   tiles each), used_pairs 1 when the pairs construction was chosen.
  *
+ * gptc_attention_block_schedule_pool(BH, nqt, per_cu, cus, wg_start, items,
+ *                                    cap, pool_j0)
+ *   The lists of the compact layout's D = 64 forward, which leaves the
+ *   blocks j < *pool_j0 of every head to a pool that workgroups whose lists
+ *   are done take from (*pool_j0 = 0: no pool, the lists hold every block).
+ *   Same filling and return as gptc_attention_block_schedule.
+ *
  * gptc_attention_key_schedule(BH, nqt, per_cu, cus, wg_start, items, cap,
  *                             est, nsplit)
  *   The work lists the D = 64 dk/dv kernel runs for BH heads of nqt 64-query
@@ -349,6 +356,8 @@ long long gptc_attention_set_state_limit(long long floats);
 long long gptc_attention_set_scratch_limit(long long floats);
 int gptc_attention_block_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
                                   double *max_cu_load, int *used_pairs);
+int gptc_attention_block_schedule_pool(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
+                                       int *pool_j0);
 int gptc_attention_key_schedule(int BH, int nqt, int per_cu, int cus, int *wg_start, int *items, int cap,
                                 double *est, int *nsplit);
 

@@ -171,6 +171,32 @@ def test_block_schedule_covers_every_block_once(lib, B, H, T):
         assert pairs and abs(load - 3 * (nqt + 1 + 1.0)) < 1e-9
 
 
+@pytest.mark.parametrize("B,H,T", [(8, 12, 1024), (4, 25, 1024), (16, 25, 1024), (1, 12, 1024), (8, 12, 320),
+                                   (8, 12, 256), (2, 3, 17), (3, 7, 2000)])
+def test_pooled_block_schedule_covers_every_block_once(lib, B, H, T):
+    """With the pool, the lists and the pool together name every (head,
+    64-query block) exactly once, and every list keeps a block (a workgroup
+    with none would count itself done without running the pool protocol's
+    first steps); where that cannot hold there is no pool."""
+    BH, nqt = B * H, (T + 63) // 64
+    cap = BH * nqt + 8 * 32 * 3 * 4 + 16
+    ws, it, j0 = (ctypes.c_int * cap)(), (ctypes.c_int * cap)(), ctypes.c_int()
+    n = lib.gptc_attention_block_schedule_pool(BH, nqt, 3, 32, ws, it, cap, ctypes.byref(j0))
+    assert n > 0
+    starts = list(ws[:n + 1])
+    items = list(it[:starts[-1]])
+    pool = [(r % BH, j0.value - 1 - r // BH) for r in range(j0.value * BH)]
+    seen = sorted([(i >> 12, i & 4095) for i in items] + pool)
+    assert seen == [(bh, j) for bh in range(BH) for j in range(nqt)]
+    if j0.value > 0:
+        assert all(b > a for a, b in zip(starts, starts[1:]))
+        assert all((i & 4095) >= j0.value for i in items)
+    if (B, H, T) == (8, 12, 1024):
+        assert j0.value == 3  # C2 runs with the pool: blocks 0, 1 and 2 of every head
+    if (B, H, T) == (2, 3, 17):
+        assert j0.value == 0  # one block per head: too few for a pool
+
+
 def test_block_schedule_balances_c5(lib):
     """C5 (100 heads x 16 blocks) has 800 pairs for 768 resident slots: the
     longest-first lists must keep every CU within 5 % of the even share."""

@@ -301,6 +301,32 @@ def test_deterministic(rt):
         assert np.array_equal(u, w)
 
 
+def test_forward_pool_over_repeated_launches(rt, oracle):
+    """C2's forward leaves blocks 0..2 of every head to a pool that workgroups
+    take from through device counters, which the last workgroup resets for
+    the next launch (block_sched.hpp).  Three launches in a row, each into an
+    output filled with NaN first, on other inputs each time: a block the
+    pool lost would leave NaN rows, a stale counter would lose the blocks of
+    the next launch.  Every launch against the oracle."""
+    lib = rt.lib
+    B, T, C, H = 8, 1024, 768, 12
+    mask = rt.from_numpy(np.tril(np.ones((T, T), np.float32)))
+    n_state = lib.gptc_attention_state_floats(B, T, C, H)
+    for launch, seed in enumerate((61, 62, 63)):
+        x = rt.normal((B, T, 3 * C), seed)
+        xt = rt.from_numpy(x)
+        yt = rt.from_numpy(np.full((B, T, C), np.nan, np.float32))
+        caches = (gptc.TensorP * 4)(xt, yt, rt.empty((B, H, T)), rt.empty((n_state,)))
+        lib.attention_forward_cuda_kernel(xt, mask, H, caches, yt)
+        y = rt.to_numpy(yt)
+        print(f"launch {launch}: seed {seed}", flush=True)
+        check("y", y, oracle.forward(x, H)[0])
+        for t in (xt, yt, caches[2], caches[3]):
+            rt.free(t)
+    rt.free(mask)
+    rt.sync()
+
+
 def test_split_key_blocks_b1_t1024(rt, oracle):
     """B*H = 12 heads of T = 1024 fill 96 of the GPU's dk/dv workgroup slots, so
     each key block with two or more query tiles runs as two workgroups over
