@@ -238,7 +238,7 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
         if (RECOMP || !half_needed(qt, qb)) return;
         const float *hb = half_base(qt, qb);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
+        for (int r = 0; r < 16; ++r) pbuf[r] = stream_load(hb + lane_off + (8 * (r >> 2) + (r & 3)) * 32);
     };
     if (qt0 < q_end) load_p(qt0, 0);
 
@@ -340,7 +340,7 @@ attn_bwd_dkdv_kernel(const BwdParams a) {
             if (!RECOMP || a.ds != nullptr) {
                 float *hb = half_base(qt, qb);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
+                for (int r = 0; r < 16; ++r) stream_store(hb + lane_off + (8 * (r >> 2) + (r & 3)) * 32, dp[r]);
             }
 
             // dV += P^T dO and dK += dS^T Q (keys x dims).
@@ -609,7 +609,7 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
         if (RECOMP || !half_needed(s, qb)) return;
         const float *hb = half_base(s, qb);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pbuf[r] = hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32];
+        for (int r = 0; r < 16; ++r) pbuf[r] = stream_load(hb + lane_off + (8 * (r >> 2) + (r & 3)) * 32);
     };
 
     f32x16 acc_dk[2], acc_dv[2];
@@ -770,7 +770,7 @@ attn_bwd_dkdv_dma_kernel(const BwdParams a) {
             {
                 float *hb = half_base(cur, qb);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) hb[lane_off + (8 * (r >> 2) + (r & 3)) * 32] = dp[r];
+                for (int r = 0; r < 16; ++r) stream_store(hb + lane_off + (8 * (r >> 2) + (r & 3)) * 32, dp[r]);
             }
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -862,7 +862,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams a) {
             const bool ok = wave_on && 32 * kb32 <= qw0 && 32 * kb32 < T;
 #pragma unroll
             for (int g = 0; g < 4; ++g)
-                dsn[kb][g] = ok ? *reinterpret_cast<const f32x4 *>(ds_tile + kb32 * kDsBlock + row_off + 8 * g)
+                dsn[kb][g] = ok ? stream_load(reinterpret_cast<const f32x4 *>(ds_tile + kb32 * kDsBlock + row_off + 8 * g))
                                 : zero4();
         }
     };
@@ -982,7 +982,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq16_kernel(const BwdParams a) {
         const uint32_t off = (16 * w + n) * 32 + 4 * j;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-            if (t < nt) dsn[t] = *reinterpret_cast<const f32x4 *>(base + (t >> 1) * kDsBlock + off + 16 * (t & 1));
+            if (t < nt) dsn[t] = stream_load(reinterpret_cast<const f32x4 *>(base + (t >> 1) * kDsBlock + off + 16 * (t & 1)));
     };
 
     int kt = 0, bh = sched_bh(a.sched.items[it]), jq = sched_j(a.sched.items[it]);

@@ -132,6 +132,20 @@ __device__ __forceinline__ f32x4 buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0));
 }
 
+// The packed P' and dS blocks are written once and read once, by the next
+// kernel: they go through these non-temporal accesses, so that they do not
+// evict from L2 and the memory-side cache the tiles that are read again
+// (the K/V prefixes of the forward, the Q/dO tiles of dk/dv, the K tiles of
+// dq) or the inputs of the next kernels.
+template <typename V>
+__device__ __forceinline__ V stream_load(const V *p) {
+    return __builtin_nontemporal_load(p);
+}
+template <typename V>
+__device__ __forceinline__ void stream_store(V *p, V v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 template <bool VEC>
 __device__ __forceinline__ void store4(float *row, int dim, int D, f32x4 v) {
     if (VEC) {

@@ -201,7 +201,7 @@ attn_fwd_kernel(const FwdParams a) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const f32x4 v = {s[kb][4 * g], s[kb][4 * g + 1], s[kb][4 * g + 2], s[kb][4 * g + 3]};
-                    *reinterpret_cast<f32x4 *>(pblk + kb * kDsBlock + prow + 8 * g) = v;
+                    stream_store(reinterpret_cast<f32x4 *>(pblk + kb * kDsBlock + prow + 8 * g), v);
                 }
             if (hf == 0 && my_q < T) a.pm[(static_cast<uint32_t>(bh) * a.nqt + kt) * T + my_q] = m_use;
         }
@@ -529,8 +529,8 @@ attn_fwd16_kernel(const FwdParams a) {
             const uint32_t prow = (16 * w + i16) * 32 + 4 * g;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb)
-                *reinterpret_cast<f32x4 *>(ptile + (kb >> 1) * kDsBlock + prow + 16 * (kb & 1)) =
-                    kb < NKB ? sc[kb] : zero4();
+                stream_store(reinterpret_cast<f32x4 *>(ptile + (kb >> 1) * kDsBlock + prow + 16 * (kb & 1)),
+                             kb < NKB ? sc[kb] : zero4());
             if (g == 0 && my_q < T) a.pm[(static_cast<uint32_t>(bh) * nqt + kt) * T + my_q] = m_use;
         }
         fwd16_pv<NKB>(v_lds, sc, g, i16, acc);
