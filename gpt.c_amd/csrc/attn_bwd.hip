@@ -25,8 +25,13 @@
 //                          recomputed from the LSE (short heads, the
 //                          LSE-only state).
 //   attn_bwd_dq16_kernel   query-parallel, D == 64: dQ += dS K, 16 queries
-//                          per wave, paired 64-query blocks per workgroup.
+//                          per wave, work lists of 64-query blocks
+//                          (block_sched.hpp).
+//   attn_bwd_dq16_recomp_kernel  the same with S and dP recomputed, for an
+//                          LSE-only state with no room for dS.
 //   attn_bwd_dq_kernel     query-parallel, other D: dQ^T += K^T dS^T.
+// P' and dS are written once and read once, through non-temporal accesses
+// (stream_load / stream_store).
 // The accumulator of the score product is directly the operand of the
 // gradient products (see the layout note in attn_common.hpp).
 #include <algorithm>
