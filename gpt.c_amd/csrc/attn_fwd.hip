@@ -7,9 +7,10 @@
 // (kernels/src/cuda/Attention.cu:170-232; math of
 // kernels/src/cpu/Attention.c:46-167).
 //
-// Two kernels.  For D == 64 with 16-byte rows (every GPT-2 shape) the
-// 16-row kernel at the end of this file runs; the 32-row kernel first below
-// serves the other head sizes.
+// Four kernels.  For D == 64 with 16-byte rows (every GPT-2 shape) the
+// 16-row kernel (attn_fwd16_kernel) runs on work lists, and short heads
+// (T <= 128) run attn_fwd_short_kernel (T <= 64) or attn_fwd_twotile_kernel;
+// the 32-row kernel first below serves the other head sizes up to 128.
 //
 // 32-row kernel: one workgroup = 4 waves = 128 queries of one (b, h); wave
 // w owns 32 queries.  The products are formed transposed, S^T = K Q^T and
