@@ -275,8 +275,15 @@ SchedTable build_with(int BH, int nqt, int per_cu, int cus, int j0) {
     best.max_cu_load = max_cu_load(best, cus);
     SchedTable lpt = lpt_schedule(BH, nqt, per_cu, cus, j0);
     lpt.max_cu_load = max_cu_load(lpt, cus);
-    // Pairs on ties: equal cost per workgroup also balances the workgroups of a CU.
-    if (lpt.max_cu_load < best.max_cu_load - 1e-9) best = std::move(lpt);
+    // Pairs on ties when they fill every resident slot: equal cost per
+    // workgroup also balances the workgroups of a CU.  With slots left over
+    // (dq16 keeps four workgroups per CU, C2 has pairs for three), lists over
+    // all the slots win up to a 2 % larger CU load: the extra workgroup's
+    // waves cover the others' waits (dq16 at C2: 55 against 54 tiles per
+    // CU, 69.8-70.2 against 70.5-71.1 us).
+    const bool pairs_fill = best.num_wg >= per_cu * cus * kSchedXcds;
+    if (lpt.max_cu_load < best.max_cu_load - 1e-9 || (!pairs_fill && lpt.max_cu_load <= 1.02 * best.max_cu_load))
+        best = std::move(lpt);
     best.pool_j0 = j0;
     return best;
 }

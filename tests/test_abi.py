@@ -197,6 +197,21 @@ def test_pooled_block_schedule_covers_every_block_once(lib, B, H, T):
         assert j0.value == 0  # one block per head: too few for a pool
 
 
+def test_block_schedule_uses_every_slot_on_ties(lib):
+    """C2's 768 pairs fill three workgroups per CU exactly; for a kernel that
+    keeps four per CU (dq16) the pairs would leave a quarter of the slots
+    empty, so the longest-first lists over all 1024 slots win while their
+    largest per-CU load is within 2 % of the pairs', and they still name
+    every block once."""
+    BH, nqt = 8 * 12, 16
+    n3, _, _, load3, pairs3 = block_schedule(lib, BH, nqt, per_cu=3)
+    n4, starts, items, load4, pairs4 = block_schedule(lib, BH, nqt, per_cu=4)
+    assert pairs3 and n3 == 768
+    assert not pairs4 and n4 == 1024 and all(b > a for a, b in zip(starts, starts[1:]))
+    assert load3 - 1e-9 <= load4 <= 1.02 * load3
+    assert sorted((i >> 12, i & 4095) for i in items) == [(bh, j) for bh in range(BH) for j in range(nqt)]
+
+
 def test_block_schedule_balances_c5(lib):
     """C5 (100 heads x 16 blocks) has 800 pairs for 768 resident slots: the
     longest-first lists must keep every CU within 5 % of the even share."""
