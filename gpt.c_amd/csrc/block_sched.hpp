@@ -10,7 +10,8 @@
 // Every (bh, j) of the problem appears exactly once in the table.
 //
 // Two ways of building it are evaluated and the one with the smaller
-// largest per-CU sum of costs is kept:
+// largest per-CU sum of costs is kept (the pairs on ties; the lpt lists
+// when the pairs leave resident slots empty and lpt is within 2 %):
 //   pairs  workgroup = blocks j and nqt-1-j of one head (equal cost nqt+1
 //          for every workgroup: ideal when the pairs fill the resident
 //          slots exactly, as at B=8, H=12, T=1024);
