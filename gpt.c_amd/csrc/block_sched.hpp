@@ -100,9 +100,9 @@ BlockSched device_block_schedule(int BH, int nqt, const void *kernel, hipStream_
 // Every other block is one item.  The items are placed like the query-block
 // lists (heads dealt to the XCDs in contiguous ranges of equal work, longest
 // first onto the least-loaded CU, then its least-loaded slot), and the CU's
-// heavier list goes to the slot dispatched first.  nsplit is the smallest
-// count whose estimated time (a CU's total, or its longest list run alone)
-// is within 2 % of the best over 0 .. nkb.
+// heavier list goes to the slot dispatched first.  nsplit is 0 when that
+// is within 5 % of the best estimated time (a CU's total, or its longest
+// list run alone) over 0 .. nkb, else the smallest count within 2 %.
 struct KeySched {
     const int *wg_start;  // num_wg + 1 offsets into items (in items, not ints)
     const int *items;     // 4 ints per item
