@@ -10,8 +10,10 @@ generate.h) must give the same logits row.  Checked here:
     gpt2_oracle.py), within 1e-4 x max(1, max|logits|), for B = 1 and B = 3;
   * C4 itself: GPT-2 124M, N(0, 0.02) init, a 64-token uniform prompt, greedy
     tokens up to T = 512: the KV-cache loop and infer_gpt.c's window loop
-    produce the same tokens, and the CPU oracle's forward over the generated
-    sequence picks every token whose top-2 logit margin exceeds 1e-3.
+    produce the same tokens, every decode step's logits match the CPU
+    oracle's 12-layer forward over the generated sequence within 1e-4 x
+    max(1, max|logits|), and that forward picks every token whose top-2
+    logit margin exceeds 1e-3.
 """
 import numpy as np
 import pytest
@@ -198,8 +200,11 @@ def test_c4_greedy_generation(rt, oracle):
         assert top2[1] - top2[0] < 1e-4, "tokens differ where the choice was not a near-tie"
     else:
         print(f"  all {total - 64} generated tokens agree")
-    # The CPU oracle over the generated sequence: teacher-forced greedy picks.
+    # The CPU oracle over the generated sequence: every decode step's logits
+    # (12 layers, positions 63 .. 510) against its forward, then the
+    # teacher-forced greedy picks.
     logits = GPT2Oracle(oracle, params, L, H).forward(kv_tokens[None, :total - 1])[0]
+    check("decode logits vs oracle (12 layers, every generated step)", kv_rows, logits[63:])
     srt = np.sort(logits[63:], axis=-1)
     margin = srt[:, -1] - srt[:, -2]
     picks = np.argmax(logits[63:], axis=-1)
