@@ -272,3 +272,49 @@ def test_key_schedule_c2_balance(lib):
         cu = (w % 8, (w // 8) % 32)
         loads[cu] = loads.get(cu, 0.0) + sum(cost(kb, qa, qe) for (bh, kb, qa, qe) in items[starts[w]:starts[w + 1]])
     assert max(loads.values()) <= 1.05 * share, (max(loads.values()), share)
+
+
+# Random shapes and occupancies: the list builders must name every block
+# exactly once whichever construction wins (pairs, longest-first lists over
+# the slots, the pool, split key blocks), or output rows would be dropped or
+# written twice.
+from hypothesis import given, settings, strategies as st
+
+
+@settings(max_examples=200, deadline=None)
+@given(BH=st.integers(1, 400), T=st.integers(1, 3000), per_cu=st.integers(1, 4), cus=st.sampled_from([1, 4, 32]))
+def test_block_schedule_property(lib, BH, T, per_cu, cus):
+    nqt = (T + 63) // 64
+    n, starts, items, load, pairs = block_schedule(lib, BH, nqt, per_cu=per_cu, cus=cus)
+    assert n % 8 == 0 and starts[0] == 0 and all(a <= b for a, b in zip(starts, starts[1:]))
+    assert sorted((i >> 12, i & 4095) for i in items) == [(bh, j) for bh in range(BH) for j in range(nqt)]
+    cap = BH * nqt + 8 * cus * per_cu * 4 + 16
+    ws, it, j0 = (ctypes.c_int * cap)(), (ctypes.c_int * cap)(), ctypes.c_int()
+    m = lib.gptc_attention_block_schedule_pool(BH, nqt, per_cu, cus, ws, it, cap, ctypes.byref(j0))
+    assert m > 0
+    pstarts = list(ws[:m + 1])
+    pool = [(r % BH, j0.value - 1 - r // BH) for r in range(j0.value * BH)]
+    seen = sorted([(i >> 12, i & 4095) for i in it[:pstarts[-1]]] + pool)
+    assert seen == [(bh, j) for bh in range(BH) for j in range(nqt)]
+    if j0.value > 0:
+        assert all(b > a for a, b in zip(pstarts, pstarts[1:]))
+
+
+@settings(max_examples=200, deadline=None)
+@given(BH=st.integers(1, 300), T=st.integers(1, 3000), per_cu=st.integers(1, 3), cus=st.sampled_from([1, 4, 32]))
+def test_key_schedule_property(lib, BH, T, per_cu, cus):
+    nqt = (T + 63) // 64
+    nkb = (nqt + 1) // 2
+    n, starts, items, est, nsplit = key_schedule(lib, BH, nqt, per_cu=per_cu, cus=cus)
+    assert n % 8 == 0 and starts[0] == 0 and all(a <= b for a, b in zip(starts, starts[1:]))
+    assert 0 <= nsplit <= nkb
+    by_block = {}
+    for bh, kb, qa, qe in items:
+        assert 0 <= bh < BH and 0 <= kb < nkb and 2 * kb <= qa < qe <= nqt
+        by_block.setdefault((bh, kb), []).append((qa, qe))
+    assert sorted(by_block) == [(bh, kb) for bh in range(BH) for kb in range(nkb)]
+    for (bh, kb), parts in by_block.items():
+        parts.sort()
+        assert parts[0][0] == 2 * kb and parts[-1][1] == nqt
+        assert all(a[1] == b[0] for a, b in zip(parts, parts[1:]))
+        assert len(parts) <= (2 if kb < nsplit else 1)
