@@ -108,26 +108,39 @@ void gptc_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, cons
 
 namespace {
 
-// out[i] += p[0][i] + p[1][i] + ... + p[S-1][i], in that order.
+// out[i] (+)= p[0][i] + p[1][i] + ... + p[S-1][i], in that order; `accumulate`
+// adds the sum to out, otherwise it overwrites out.
 __global__ __launch_bounds__(kThreads) void add_partials_kernel(const float *__restrict__ p, float *__restrict__ out,
-                                                               int64_t n, int S, bool vec) {
+                                                               int64_t n, int S, bool vec, bool accumulate) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
     if (vec) {
         const int64_t n4 = n / 4;
         for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
             f32x4 acc = reinterpret_cast<const f32x4 *>(p)[i];
             for (int s = 1; s < S; ++s) acc += reinterpret_cast<const f32x4 *>(p + s * n)[i];
-            f32x4 o = reinterpret_cast<f32x4 *>(out)[i];
-            o += acc;
-            reinterpret_cast<f32x4 *>(out)[i] = o;
+            if (accumulate) {
+                f32x4 o = reinterpret_cast<f32x4 *>(out)[i];
+                o += acc;
+                acc = o;
+            }
+            reinterpret_cast<f32x4 *>(out)[i] = acc;
         }
     } else {
         for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
             float acc = p[i];
             for (int s = 1; s < S; ++s) acc += p[s * n + i];
-            out[i] += acc;
+            out[i] = accumulate ? out[i] + acc : acc;
         }
     }
+}
+
+void launch_add_partials(const float *partial, float *out, int64_t n, int S, bool accumulate, hipStream_t s) {
+    int64_t blocks = (n / 4 + kThreads - 1) / kThreads;
+    if (blocks > 256 * 8) blocks = 256 * 8;
+    const bool vec = (n % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    add_partials_kernel<<<dim3(static_cast<int>(blocks < 1 ? 1 : blocks)), dim3(kThreads), 0, s>>>(partial, out, n, S,
+                                                                                                   vec, accumulate);
+    hipCheck(hipGetLastError());
 }
 
 }  // namespace
@@ -155,12 +168,44 @@ void gptc_sgemm_wgrad(int out_f, int in_f, int rows, const float *g, const float
                                              static_cast<rocblas_stride>(chunk) * in_f, g, out_f,
                                              static_cast<rocblas_stride>(chunk) * out_f, &zero, partial, in_f, n, S),
                "sgemm_strided_batched (weight gradient)");
-    int64_t blocks = (n / 4 + kThreads - 1) / kThreads;
-    if (blocks > 256 * 8) blocks = 256 * 8;
-    const bool vec = (n % 4) == 0 && (reinterpret_cast<uintptr_t>(dW) & 15) == 0;
-    add_partials_kernel<<<dim3(static_cast<int>(blocks < 1 ? 1 : blocks)), dim3(kThreads), 0, s>>>(partial, dW, n, S,
-                                                                                                   vec);
-    hipCheck(hipGetLastError());
+    launch_add_partials(partial, dW, n, S, true, s);
+    free_cuda(partial);
+}
+
+void gptc_sgemm_dgrad(int rows, int in_f, int out_f, const float *g, const float *W, float *dx) {
+    if (rows <= 0 || in_f <= 0) return;
+    // With rocBLAS's atomics off, a product with few 128 x 128 output tiles and
+    // a long reduction runs on one wave of tiles with a third of the CUs idle
+    // (GPT-2's lm_head input gradient: 384 tiles, K = 50257, 113 TFLOP/s).  The
+    // reduction is then split into S equal slices, as in the weight gradient,
+    // while every slice keeps at least 8192 terms: below that the extra passes
+    // over the slices cost more than the fuller GPU gains (measured at K = 2304
+    // and 3072).  The K - S*chunk leftover terms are added into slice 0.
+    const int64_t tiles = static_cast<int64_t>((rows + 127) / 128) * ((in_f + 127) / 128);
+    int S = 1;
+    while (S < 8 && tiles * S < 512 && out_f / (2 * S) >= 8192) S *= 2;
+    if (S == 1) {
+        gptc_sgemm(0, 0, rows, in_f, out_f, 1.0f, g, out_f, W, in_f, 0.0f, dx, in_f);
+        return;
+    }
+    hipStream_t s = gptc_stream_checked();
+    const int chunk = out_f / S, rest = out_f - S * chunk;
+    const int64_t n = static_cast<int64_t>(rows) * in_f;
+    float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * static_cast<size_t>(n) * S));
+    const float one = 1.0f, zero = 0.0f;
+    // Column-major view: partial_b^T (in x rows) = W_b^T (in x chunk) g_b^T (chunk x rows),
+    // W_b = rows [b*chunk, (b+1)*chunk) of W, g_b = the same columns of g.
+    blas_check(rocblas_sgemm_strided_batched(gptc_blas_handle(), rocblas_operation_none, rocblas_operation_none, in_f,
+                                             rows, chunk, &one, W, in_f, static_cast<rocblas_stride>(chunk) * in_f, g,
+                                             out_f, chunk, &zero, partial, in_f, n, S),
+               "sgemm_strided_batched (input gradient)");
+    if (rest > 0) {
+        const int64_t k0 = static_cast<int64_t>(S) * chunk;
+        blas_check(rocblas_sgemm(gptc_blas_handle(), rocblas_operation_none, rocblas_operation_none, in_f, rows, rest,
+                                 &one, W + k0 * in_f, in_f, g + k0, out_f, &one, partial, in_f),
+                   "sgemm (input gradient, leftover terms)");
+    }
+    launch_add_partials(partial, dx, n, S, false, s);
     free_cuda(partial);
 }
 

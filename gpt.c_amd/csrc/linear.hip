@@ -254,8 +254,8 @@ extern "C" void linear_backward_cuda_kernel(const tensor_t *global_grad, const t
         CHECK_ERROR(db->length != out_f, "Expected db to hold %d elements, but got %d.", out_f, db->length);
     }
     hipStream_t s = gptc_stream_checked();
-    // dx = g W : (rows x out) (out x in)
-    gptc_sgemm(0, 0, rows, in_f, out_f, 1.0f, global_grad->t, out_f, W->t, in_f, 0.0f, dout->t, in_f);
+    // dx = g W : (rows x out) (out x in), split over out when the reduction is long and the output small
+    gptc_sgemm_dgrad(rows, in_f, out_f, global_grad->t, W->t, dout->t);
     // dW += g^T x : (out x rows) (rows x in), split over rows when the output is small
     gptc_sgemm_wgrad(out_f, in_f, rows, global_grad->t, cache->t, dW->t);
     if (db != NULL) launch_column_sum_add(global_grad->t, db->t, rows, out_f, s);

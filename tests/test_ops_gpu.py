@@ -82,6 +82,9 @@ def dev(rt):
     (4, 256, 768, 3072, True),   # GPT-2 c_fc
     (2, 128, 3072, 768, True),   # GPT-2 mlp c_proj
     (1, 64, 768, 2304, True),    # GPT-2 qkv
+    (2, 64, 768, 50257, False),  # GPT-2 lm_head: dx split over 4 slices of 12564 terms + 1 leftover term
+    (1, 3, 7, 16391, True),      # dx split over 2 slices + 1 leftover term, scalar (in_f % 4 != 0) add
+    (1, 16, 64, 32768, True),    # dx split over 4 slices, no leftover terms
 ])
 def test_linear(dev, ops, B, T, in_f, out_f, bias):
     print(f"case linear B={B} T={T} in={in_f} out={out_f} bias={bias}")
