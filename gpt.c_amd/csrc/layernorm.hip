@@ -72,11 +72,12 @@ __global__ __launch_bounds__(kThreads) void layernorm_fwd_kernel(const float *__
 
 // Workgroup blockIdx.x owns rows [r0, r1); its waves take every 4th row.
 // partial: (2, gridDim.x, C) = dW then db sums of this workgroup.
+// acc: dout += dx (the reference's semantics); otherwise dout = dx.
 template <int K>
 __global__ __launch_bounds__(kThreads) void layernorm_bwd_kernel(
     const float *__restrict__ g, const float *__restrict__ x, const float *__restrict__ mean_in,
     const float *__restrict__ rstd_in, const float *__restrict__ W, float *__restrict__ dout,
-    float *__restrict__ partial, int rows, int C, int rows_per_block) {
+    float *__restrict__ partial, int rows, int C, int rows_per_block, bool acc) {
     extern __shared__ float red[];  // (kWaves, 2, C)
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     const int r0 = blockIdx.x * rows_per_block;
@@ -116,7 +117,8 @@ __global__ __launch_bounds__(kThreads) void layernorm_bwd_kernel(
             if (j < C) {
                 dw[k] += gv[k] * (a * xv[k] + bn);
                 dbs[k] += gv[k];
-                dr[j] += a * gv[k] * wv[k] + bb * xv[k] + cc;
+                const float d = a * gv[k] * wv[k] + bb * xv[k] + cc;
+                dr[j] = acc ? dr[j] + d : d;
             }
         }
     }
@@ -126,6 +128,118 @@ __global__ __launch_bounds__(kThreads) void layernorm_bwd_kernel(
         if (j < C) {
             red[(w * 2 + 0) * C + j] = dw[k];
             red[(w * 2 + 1) * C + j] = dbs[k];
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < C; j += kThreads) {
+        float sw = red[j], sb = red[C + j];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) {
+            sw += red[(i * 2 + 0) * C + j];
+            sb += red[(i * 2 + 1) * C + j];
+        }
+        partial[static_cast<int64_t>(blockIdx.x) * C + j] = sw;
+        partial[(static_cast<int64_t>(gridDim.x) + blockIdx.x) * C + j] = sb;
+    }
+}
+
+// The same backward on float4 columns (C % 4 == 0, 16-byte aligned rows and
+// W): lane l holds float4 columns l, l + 64, ...  A wave takes ROWS of its
+// rows per step (r, r + 4, ...) and issues every load of them, dout's
+// included, before the first use, so a step costs one memory latency.
+// ACC: dout += dx (the reference's semantics); otherwise dout = dx and
+// dout is not read.  The dW / db sums of a column see the rows in the same
+// order as in the kernel above.
+template <int K4, int ROWS, bool ACC>
+__global__ __launch_bounds__(kThreads) void layernorm_bwd4_kernel(
+    const float *__restrict__ g, const float *__restrict__ x, const float *__restrict__ mean_in,
+    const float *__restrict__ rstd_in, const float *__restrict__ W, float *__restrict__ dout,
+    float *__restrict__ partial, int rows, int C, int rows_per_block) {
+    extern __shared__ float red[];  // (kWaves, 2, C)
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int n4 = C / 4;
+    const int r0 = blockIdx.x * rows_per_block;
+    const int r1 = min(rows, r0 + rows_per_block);
+    const float scale = 1.0f / C;
+    const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4_t wv[K4], dw[K4], dbs[K4];
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int c = lane + k * kWave;
+        wv[k] = c < n4 ? reinterpret_cast<const f32x4_t *>(W)[c] : zero;
+        dw[k] = zero;
+        dbs[k] = zero;
+    }
+    for (int row = r0 + w; row < r1; row += ROWS * kWaves) {
+        f32x4_t xv[ROWS][K4], gv[ROWS][K4], ov[ROWS][K4];
+        float mean[ROWS], a[ROWS];
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            // A row past r1 repeats row's loads; its results are not used.
+            const int ri = min(row + i * kWaves, r1 - 1);
+            const f32x4_t *xr = reinterpret_cast<const f32x4_t *>(x + static_cast<int64_t>(ri) * C);
+            const f32x4_t *gr = reinterpret_cast<const f32x4_t *>(g + static_cast<int64_t>(ri) * C);
+            const f32x4_t *dr = reinterpret_cast<const f32x4_t *>(dout + static_cast<int64_t>(ri) * C);
+#pragma unroll
+            for (int k = 0; k < K4; ++k) {
+                const int c = min(lane + k * kWave, n4 - 1);
+                xv[i][k] = xr[c];
+                gv[i][k] = gr[c];
+                if (ACC) ov[i][k] = dr[c];
+            }
+            mean[i] = mean_in[ri];
+            a[i] = rstd_in[ri];
+        }
+        float ds[ROWS], dbacc[ROWS];
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            ds[i] = 0.0f;
+            dbacc[i] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K4; ++k) {
+                if (lane + k * kWave >= n4) {  // the clamped loads above: not this lane's columns
+                    xv[i][k] = zero;
+                    gv[i][k] = zero;
+                }
+                const f32x4_t gw = gv[i][k] * wv[k];
+                const f32x4_t gxw = gw * xv[i][k];
+                ds[i] += (gxw[0] + gxw[1]) + (gxw[2] + gxw[3]);
+                dbacc[i] += (gw[0] + gw[1]) + (gw[2] + gw[3]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            ds[i] = wave_sum(ds[i]);
+            dbacc[i] = wave_sum(dbacc[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+            const int r = row + i * kWaves;
+            if (i > 0 && r >= r1) break;
+            const float m = mean[i], ai = a[i];
+            const float bn = -ai * m;
+            const float bb = (dbacc[i] * m - ds[i]) * ai * ai * ai * scale;
+            const float cc = -bb * m - dbacc[i] * ai * scale;
+            f32x4_t *dr = reinterpret_cast<f32x4_t *>(dout + static_cast<int64_t>(r) * C);
+#pragma unroll
+            for (int k = 0; k < K4; ++k) {
+                const int c = lane + k * kWave;
+                if (c < n4) {
+                    dw[k] += gv[i][k] * (ai * xv[i][k] + bn);
+                    dbs[k] += gv[i][k];
+                    const f32x4_t d = ai * gv[i][k] * wv[k] + bb * xv[i][k] + cc;
+                    dr[c] = ACC ? ov[i][k] + d : d;
+                }
+            }
+        }
+    }
+    f32x4_t *red4 = reinterpret_cast<f32x4_t *>(red);
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int c = lane + k * kWave;
+        if (c < n4) {
+            red4[(w * 2 + 0) * n4 + c] = dw[k];
+            red4[(w * 2 + 1) * n4 + c] = dbs[k];
         }
     }
     __syncthreads();
@@ -176,13 +290,51 @@ struct FwdLaunch {
 template <int K>
 struct BwdLaunch {
     static void run(const float *g, const float *x, const float *mean, const float *rstd, const float *W, float *dout,
-                    float *partial, int rows, int C, int parts, int rows_per_block, hipStream_t s) {
+                    float *partial, int rows, int C, int parts, int rows_per_block, bool acc, hipStream_t s) {
         const size_t lds = sizeof(float) * kWaves * 2 * C;
         layernorm_bwd_kernel<K><<<dim3(parts), dim3(kThreads), lds, s>>>(g, x, mean, rstd, W, dout, partial, rows, C,
-                                                                        rows_per_block);
+                                                                        rows_per_block, acc);
         hipCheck(hipGetLastError());
     }
 };
+
+// Float4 columns per lane of layernorm_bwd4_kernel: 1, 2, 3, 4, 6 or 8
+// (C <= 256, 512, 768, 1024, 1536, 2048); two rows per step up to 4.
+template <int K4>
+void bwd4_launch(const float *g, const float *x, const float *mean, const float *rstd, const float *W, float *dout,
+                 float *partial, int rows, int C, int parts, int rows_per_block, bool acc, hipStream_t s) {
+    constexpr int R = K4 <= 4 ? 2 : 1;
+    const size_t lds = sizeof(float) * kWaves * 2 * C;
+    if (acc)
+        layernorm_bwd4_kernel<K4, R, true><<<dim3(parts), dim3(kThreads), lds, s>>>(g, x, mean, rstd, W, dout,
+                                                                                   partial, rows, C, rows_per_block);
+    else
+        layernorm_bwd4_kernel<K4, R, false><<<dim3(parts), dim3(kThreads), lds, s>>>(g, x, mean, rstd, W, dout,
+                                                                                    partial, rows, C, rows_per_block);
+    hipCheck(hipGetLastError());
+}
+
+// dout (+)= dx, dW += ..., db += ... of rows x C (1 <= C <= kMaxCols).
+void layer_norm_backward(const float *g, const float *x, const float *mean, const float *rstd, const float *W,
+                         float *dout, float *dW, float *db, int rows, int C, bool acc, hipStream_t s) {
+    // About 4 rows per wave: 512 workgroups (two per CU) at GPT-2's 8192 rows.
+    int parts = (rows + 15) / 16;
+    if (parts > 1024) parts = 1024;
+    const int rows_per_block = (rows + parts - 1) / parts;
+    parts = (rows + rows_per_block - 1) / rows_per_block;
+    float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * 2 * static_cast<size_t>(parts) * C));
+    if (C % 4 == 0 && aligned16(g) && aligned16(x) && aligned16(W) && aligned16(dout)) {
+        const int k4 = (C / 4 + kWave - 1) / kWave;
+        auto f = k4 <= 1 ? bwd4_launch<1> : k4 <= 2 ? bwd4_launch<2> : k4 <= 3 ? bwd4_launch<3>
+               : k4 <= 4 ? bwd4_launch<4> : k4 <= 6 ? bwd4_launch<6> : bwd4_launch<8>;
+        f(g, x, mean, rstd, W, dout, partial, rows, C, parts, rows_per_block, acc, s);
+    } else {
+        by_cols<BwdLaunch>(C, g, x, mean, rstd, W, dout, partial, rows, C, parts, rows_per_block, acc, s);
+    }
+    launch_add_column_partials(partial, dW, parts, C, s);
+    if (db != nullptr) launch_add_column_partials(partial + static_cast<size_t>(parts) * C, db, parts, C, s);
+    free_cuda(partial);
+}
 
 void check_cols(int C) {
     CHECK_ERROR(C < 1 || C > kMaxCols, "LayerNorm supports 1 .. %d features, but got %d.", kMaxCols, C);
@@ -218,8 +370,10 @@ extern "C" void layer_norm_forward_cuda_kernel(const tensor_t *W, const tensor_t
                        rows, C, eps, s);
 }
 
-extern "C" void layer_norm_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t **cache,
-                                                const tensor_t *W, tensor_t *dW, tensor_t *db, tensor_t *dout) {
+namespace {
+
+void layer_norm_backward_checked(const tensor_t *global_grad, const tensor_t **cache, const tensor_t *W, tensor_t *dW,
+                                 tensor_t *db, tensor_t *dout, bool acc) {
     check_gpu(global_grad, "global_grad");
     REQUIRE_ARG(cache);
     check_gpu(cache[0], "cache[0] (mean)");
@@ -239,17 +393,18 @@ extern "C" void layer_norm_backward_cuda_kernel(const tensor_t *global_grad, con
         CHECK_ERROR(db->length != C, "Expected db to hold %d elements, but got %d.", C, db->length);
     }
     if (rows == 0) return;
-    hipStream_t s = gptc_stream_checked();
-    // About 4 rows per wave: 512 workgroups (two per CU) at GPT-2's 8192 rows.
-    int parts = (rows + 15) / 16;
-    if (parts > 1024) parts = 1024;
-    const int rows_per_block = (rows + parts - 1) / parts;
-    parts = (rows + rows_per_block - 1) / rows_per_block;
-    float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * 2 * static_cast<size_t>(parts) * C));
-    by_cols<BwdLaunch>(C, static_cast<const float *>(global_grad->t), static_cast<const float *>(cache[2]->t),
-                       static_cast<const float *>(cache[0]->t), static_cast<const float *>(cache[1]->t),
-                       static_cast<const float *>(W->t), dout->t, partial, rows, C, parts, rows_per_block, s);
-    launch_add_column_partials(partial, dW->t, parts, C, s);
-    if (db != NULL) launch_add_column_partials(partial + static_cast<size_t>(parts) * C, db->t, parts, C, s);
-    free_cuda(partial);
+    layer_norm_backward(global_grad->t, cache[2]->t, cache[0]->t, cache[1]->t, W->t, dout->t, dW->t,
+                        db != NULL ? db->t : nullptr, rows, C, acc, gptc_stream_checked());
+}
+
+}  // namespace
+
+extern "C" void layer_norm_backward_cuda_kernel(const tensor_t *global_grad, const tensor_t **cache,
+                                                const tensor_t *W, tensor_t *dW, tensor_t *db, tensor_t *dout) {
+    layer_norm_backward_checked(global_grad, cache, W, dW, db, dout, true);
+}
+
+extern "C" void gptc_layer_norm_backward_set(const tensor_t *global_grad, const tensor_t **cache, const tensor_t *W,
+                                             tensor_t *dW, tensor_t *db, tensor_t *dout) {
+    layer_norm_backward_checked(global_grad, cache, W, dW, db, dout, false);
 }

@@ -5,6 +5,8 @@
 // dW's GEMM has a small output (out x in) and a long reduction (B*T rows):
 // it is split over row slices (one strided-batched GEMM) and the slices are
 // added into dW in a fixed order, so it fills the GPU and stays deterministic.
+// dx's GEMM is split the same way over its reduction (out features) when that
+// is long and the output small: GPT-2's lm_head (K = 50257, 8192 x 768).
 // The column sums are deterministic: workgroups sum fixed row ranges into a
 // partial buffer, and a second kernel adds the partials in a fixed order
 // (the reference uses one atomicAdd per workgroup and column); float4

@@ -184,6 +184,7 @@ SIGNATURES = {
     "layer_norm_forward_cuda_kernel": (None, [TensorP, TensorP, TensorP, _cf, ctypes.POINTER(TensorP), TensorP]),
     "layer_norm_backward_cuda_kernel": (None, [TensorP, ctypes.POINTER(TensorP), TensorP, TensorP, TensorP,
                                                TensorP]),
+    "gptc_layer_norm_backward_set": (None, [TensorP, ctypes.POINTER(TensorP), TensorP, TensorP, TensorP, TensorP]),
     "gelu_forward_cuda_kernel": (None, [TensorP, TensorP]),
     "gelu_backward_cuda_kernel": (None, [TensorP, TensorP, TensorP]),
     "softmax_forward_cuda_kernel": (None, [TensorP, TensorP]),

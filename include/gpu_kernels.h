@@ -122,6 +122,17 @@ void gptc_attention_backward_qkv_bias(const tensor_t *global_grad, tensor_t **ca
                                       const int n_heads, tensor_t *dout, tensor_t *db);
 
 /*
+ * gptc_layer_norm_backward_set(global_grad, cache, W, dW, db, dout)
+ *   As layer_norm_backward_cuda_kernel, but dout = dx instead of dout += dx
+ *   (dout is not read).  No counterpart in the reference: gpt.c's LayerNorm
+ *   layer zero-fills a new dout before the accumulating kernel
+ *   (src/layer_norm.c:127-135); the layer here calls this and skips the fill
+ *   and the read of the zeros (50 MB per call at GPT-2 small's B=8 T=1024).
+ */
+void gptc_layer_norm_backward_set(const tensor_t *global_grad, const tensor_t **cache, const tensor_t *W,
+                                  tensor_t *dW, tensor_t *db, tensor_t *dout);
+
+/*
  * ---- the rest of gpt.c's GPU back end (the other layers of the model) ----
  * Same names, arguments and meaning as the CUDA entry points they replace;
  * the semantics are those of gpt.c's CPU kernels (kernels/src/cpu/), which

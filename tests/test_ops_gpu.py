@@ -125,6 +125,15 @@ def test_layer_norm(dev, ops, B, T, C):
     check("dx (accumulated)", dev.get(dx_t), dx, atol=2e-5)
     check("dW (accumulated)", dev.get(dW_t), dW, rtol=2e-6, atol=2e-5)
     check("db (accumulated)", dev.get(db_t), db, rtol=2e-6, atol=2e-5)
+    # The layer's form writes dx over whatever dout holds (NaN here) and
+    # still accumulates dW and db.
+    dx_set = dev(np.full((B, T, C), np.nan, np.float32))
+    dev.rt.lib.gptc_layer_norm_backward_set(dev(g), cache3, dev(W), dW_t, db_t, dx_set)
+    dx2 = np.zeros_like(dx0)
+    ops.layer_norm_backward(g, x, m_ref, r_ref, W, dW, db, dx2)
+    check("dx (written)", dev.get(dx_set), dx2, atol=2e-5)
+    check("dW (accumulated twice)", dev.get(dW_t), dW, rtol=2e-6, atol=4e-5)
+    check("db (accumulated twice)", dev.get(db_t), db, rtol=2e-6, atol=4e-5)
 
 
 def test_layer_norm_without_bias(dev, ops):
