@@ -4,11 +4,13 @@
 //   forward   cache[0] = log_softmax(logits) per row; output[0] = mean over
 //             rows of -log_softmax[target];
 //   backward  with s = -g / (B T):  dout[j] = [j == target] s - exp(lsm[j]) s.
-// A row is one 256-thread workgroup: one online (max, sum) pass over the
-// logits, then a pass that writes the log-softmax (float4 accesses and exp2
-// where the buffers are 16-byte aligned).  The per-row losses go to
-// a buffer and one workgroup adds them in a fixed order, so the mean is
-// deterministic.  A target outside [0, V) makes that row's loss NaN (the
+// A row is one workgroup.  Rows of up to 65536 logits (16-byte aligned
+// buffers) are held in the registers of a 512-thread workgroup: one read of
+// the logits, then the max, the sum and the log-softmax from registers.
+// Longer rows take one online (max, sum) pass over the logits, then a pass
+// that writes the log-softmax (float4 accesses and exp2 where aligned).
+// The per-row losses go to a buffer and one workgroup adds them in a fixed
+// order, so the mean is deterministic.  A target outside [0, V) makes that row's loss NaN (the
 // reference would read outside the row) and its gradient row is the softmax
 // part only.
 #include "gpu_kernels.h"
@@ -195,6 +197,128 @@ __global__ __launch_bounds__(kThreads) void ce_bwd4_kernel(const float *__restri
     if (je >= 0) dr[je] = (je == t ? s : 0.0f) - __builtin_amdgcn_exp2f(lr[je] * kLog2eF) * s;
 }
 
+// Row-resident forms of the two kernels for rows of at most 512 NPT float4
+// (GPT-2's V = 50257 takes NPT = 25): a 512-thread workgroup issues every
+// load of its row before the first use and keeps the row in registers, so
+// the forward reads the logits once (max, then the sum of exponentials, then
+// the output, all from registers; 8 V bytes per row instead of 12 V) and
+// the backward's loads are not held behind its stores.
+constexpr int kRowThreads = 512;
+constexpr int kRowWaves = kRowThreads / kWave;
+
+// Block-wide max / sum of one value per thread (sum in wave order, fixed).
+__device__ __forceinline__ float row_max(float v, float *red) {
+    v = wave_max(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kRowWaves; ++i) r = fmaxf(r, red[i]);
+    __syncthreads();  // red is reused by the next reduction
+    return r;
+}
+__device__ __forceinline__ float row_sum(float v, float *red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kRowWaves; ++i) r += red[i];
+    return r;
+}
+
+template <int NPT>
+__global__ __launch_bounds__(kRowThreads) void ce_fwd_row_kernel(const float *__restrict__ logits,
+                                                                const float *__restrict__ targets,
+                                                                float *__restrict__ lsm, float *__restrict__ row_loss,
+                                                                int V) {
+    __shared__ float red[kRowWaves];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * V;
+    const float *xr = logits + base;
+    int head, n4;
+    row_split(base, V, head, n4);
+    const int je = row_end_index(head, head + 4 * n4, V);
+    const f32x4_t *x4 = reinterpret_cast<const f32x4_t *>(xr + head);
+    const f32x4_t ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    f32x4_t v[NPT];
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const int i = threadIdx.x + k * kRowThreads;
+        v[k] = i < n4 ? x4[i] : ninf;
+    }
+    const float ve = je >= 0 ? xr[je] : -INFINITY;
+    float mx = ve;
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) mx = fmaxf(mx, fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])));
+    const float M = row_max(mx, red);
+    // exp(x - M) = exp2(x log2(e) - M log2(e)); a row of -inf only sums to 0.
+    const float ml2 = M == -INFINITY ? 0.0f : M * kLog2eF;
+    float s = __builtin_amdgcn_exp2f(fmaf(ve, kLog2eF, -ml2));
+#pragma unroll
+    for (int k = 0; k < NPT; ++k)
+        s += (__builtin_amdgcn_exp2f(fmaf(v[k][0], kLog2eF, -ml2)) + __builtin_amdgcn_exp2f(fmaf(v[k][1], kLog2eF, -ml2))) +
+             (__builtin_amdgcn_exp2f(fmaf(v[k][2], kLog2eF, -ml2)) + __builtin_amdgcn_exp2f(fmaf(v[k][3], kLog2eF, -ml2)));
+    const float S = row_sum(s, red);
+    const float shift = M + logf(S);  // log of the row's sum of exp
+    float *lr = lsm + base;
+    f32x4_t *l4 = reinterpret_cast<f32x4_t *>(lr + head);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const int i = threadIdx.x + k * kRowThreads;
+        if (i < n4) l4[i] = v[k] - shift;
+    }
+    if (je >= 0) lr[je] = ve - shift;
+    if (threadIdx.x == 0) {
+        const int t = static_cast<int>(targets[blockIdx.x]);
+        row_loss[blockIdx.x] = (t >= 0 && t < V) ? -(xr[t] - shift) : NAN;
+    }
+}
+
+template <int NPT>
+__global__ __launch_bounds__(kRowThreads) void ce_bwd_row_kernel(const float *__restrict__ g,
+                                                                const float *__restrict__ lsm,
+                                                                const float *__restrict__ targets,
+                                                                float *__restrict__ dout, int V, float rows_f) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * V;
+    const float s = -g[blockIdx.x] / rows_f;
+    const int t = static_cast<int>(targets[blockIdx.x]);
+    int head, n4;
+    row_split(base, V, head, n4);
+    const int je = row_end_index(head, head + 4 * n4, V);
+    const float *lr = lsm + base;
+    float *dr = dout + base;
+    const f32x4_t *l4 = reinterpret_cast<const f32x4_t *>(lr + head);
+    f32x4_t *d4 = reinterpret_cast<f32x4_t *>(dr + head);
+    f32x4_t l[NPT];
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const int i = threadIdx.x + k * kRowThreads;
+        l[k] = i < n4 ? l4[i] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const float le = je >= 0 ? lr[je] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const int i = threadIdx.x + k * kRowThreads;
+        if (i < n4) {
+            f32x4_t d;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                d[c] = (head + 4 * i + c == t ? s : 0.0f) - __builtin_amdgcn_exp2f(l[k][c] * kLog2eF) * s;
+            d4[i] = d;
+        }
+    }
+    if (je >= 0) dr[je] = (je == t ? s : 0.0f) - __builtin_amdgcn_exp2f(le * kLog2eF) * s;
+}
+
+// NPT for a row of n4 float4 (0: too long, use the streaming kernels).
+int row_npt(int V) {
+    const int n4 = V / 4;
+    if (n4 <= 8 * kRowThreads) return 8;
+    if (n4 <= 25 * kRowThreads) return 25;
+    if (n4 <= 32 * kRowThreads) return 32;
+    return 0;
+}
+
 }  // namespace
 
 }  // namespace gptc
@@ -216,7 +340,11 @@ extern "C" void cross_entropy_forward_cuda_kernel(const tensor_t *logits, const 
     CHECK_ERROR(rows < 1 || V < 1, "Expected at least one row of logits.");
     hipStream_t s = gptc_stream_checked();
     float *row_loss = static_cast<float *>(alloc_cuda(sizeof(float) * rows));
-    if (aligned16(logits->t) && aligned16(cache[0]->t))
+    const int npt = row_npt(V);
+    if (aligned16(logits->t) && aligned16(cache[0]->t) && npt > 0) {
+        auto k = npt == 8 ? ce_fwd_row_kernel<8> : npt == 25 ? ce_fwd_row_kernel<25> : ce_fwd_row_kernel<32>;
+        k<<<dim3(rows), dim3(kRowThreads), 0, s>>>(logits->t, targets->t, cache[0]->t, row_loss, V);
+    } else if (aligned16(logits->t) && aligned16(cache[0]->t))
         ce_fwd4_kernel<<<dim3(rows), dim3(kThreads), 0, s>>>(logits->t, targets->t, cache[0]->t, row_loss, V);
     else
         ce_fwd_kernel<<<dim3(rows), dim3(kThreads), 0, s>>>(logits->t, targets->t, cache[0]->t, row_loss, V);
@@ -240,7 +368,12 @@ extern "C" void cross_entropy_backward_cuda_kernel(const tensor_t *global_grad, 
     CHECK_ERROR(dout->length != lsm->length, "Expected dout to match the logits' %d elements.", lsm->length);
     if (rows == 0) return;
     // The reference divides by the int B*T (cpu/CrossEntropyLoss.c:67-72).
-    if (aligned16(lsm->t) && aligned16(dout->t))
+    const int npt = row_npt(V);
+    if (aligned16(lsm->t) && aligned16(dout->t) && npt > 0) {
+        auto k = npt == 8 ? ce_bwd_row_kernel<8> : npt == 25 ? ce_bwd_row_kernel<25> : ce_bwd_row_kernel<32>;
+        k<<<dim3(rows), dim3(kRowThreads), 0, gptc_stream_checked()>>>(global_grad->t, lsm->t, cache[1]->t, dout->t,
+                                                                       V, static_cast<float>(rows));
+    } else if (aligned16(lsm->t) && aligned16(dout->t))
         ce_bwd4_kernel<<<dim3(rows), dim3(kThreads), 0, gptc_stream_checked()>>>(
             global_grad->t, lsm->t, cache[1]->t, dout->t, V, static_cast<float>(rows));
     else

@@ -228,6 +228,35 @@ def test_cross_entropy(dev, ops, B, T, V):
     check("dlogits", dev.get(d), ops.cross_entropy_backward(g, lsm_ref, tg), atol=1e-7)
 
 
+@pytest.mark.parametrize("B,T,V", [(2, 3, 8 * 2048 + 3), (2, 2, 8 * 2048 + 5), (1, 3, 25 * 2048 + 3),
+                                   (2, 2, 32 * 2048 + 1), (1, 2, 70001)])
+def test_cross_entropy_row_sizes_and_masked_logits(dev, ops, B, T, V):
+    """Rows at the edges of the register-resident forms (8, 25 and 32 float4
+    per lane) and one longer row (the streaming kernels), with -inf logits
+    (masked entries) in every row and one row masked but for its target."""
+    print(f"case cross_entropy rows B={B} T={T} V={V}")
+    logits = rnd(B, T, V, scale=2.0)
+    logits[..., 7::13] = -np.inf
+    tg = RNG.integers(0, V, (B, T)).astype(np.float32)
+    tg = np.where(tg % 13 == 7, tg - 1, tg)  # targets on unmasked entries
+    logits[0, 0, :] = -np.inf
+    logits[0, 0, int(tg[0, 0])] = 3.0
+    lsm, loss = dev.empty((B, T, V)), dev.empty((1,))
+    tg_t = dev(tg)
+    dev.rt.lib.cross_entropy_forward_cuda_kernel(dev(logits), tg_t, (gptc.TensorP * 1)(lsm), loss)
+    lsm_ref, loss_ref = ops.cross_entropy_forward(logits, tg)
+    got = dev.get(lsm)
+    assert np.array_equal(np.isneginf(got), np.isneginf(lsm_ref))
+    fin = np.isfinite(lsm_ref)
+    check("log-softmax (finite entries)", got[fin], lsm_ref[fin], atol=1e-4)
+    assert abs(got[0, 0, int(tg[0, 0])]) <= 1e-6  # the only unmasked logit of its row
+    check("loss", dev.get(loss), np.array([loss_ref]), atol=1e-4)
+    g = rnd(B, T)
+    d = dev.empty((B, T, V))
+    dev.rt.lib.cross_entropy_backward_cuda_kernel(dev(g), (gptc.TensorP * 2)(dev(lsm_ref), tg_t), d)
+    check("dlogits", dev.get(d), ops.cross_entropy_backward(g, lsm_ref, tg), atol=1e-7)
+
+
 def test_cross_entropy_uniform_logits_and_bad_target(dev):
     B, T, V = 2, 3, 50257
     logits = np.zeros((B, T, V), np.float32)
