@@ -5,9 +5,26 @@
 #pragma once
 
 #include <stdlib.h>
+#include <string.h>
 #include "dispatch.h"
+#include "gpu_kernels.h"
 #include "tensor.h"
 #include "utils.h"
+
+/* A second tensor_t over t's GPU storage: the block gains an owner
+ * (gptc_retain_cuda) and returns to the allocator when both are freed.
+ * Writes through either are seen by both.  Other tensors are copied. */
+static inline tensor_t *share_tensor(const tensor_t *t) {
+    if (t->device != CUDA || t->t == NULL) {
+        tensor_t *c = create_tensor(t->shape, t->ndims, t->device);
+        tensor_copy(c, t);
+        return c;
+    }
+    tensor_t *s = (tensor_t *)mallocCheck(sizeof(tensor_t));
+    memcpy(s, t, sizeof(tensor_t));
+    gptc_retain_cuda(t->t);
+    return s;
+}
 
 /* Move a tensor if it exists. */
 static inline void move_opt(tensor_t *t, const device_t device) {
