@@ -166,6 +166,10 @@ SIGNATURES = {
     "gptc_attention_backward_bias": (TensorP, [_vp, TensorP, TensorP, TensorP]),
     "gptc_linear_forward_nobias": (TensorP, [_vp, TensorP]),
     "gptc_linear_backward_nodb": (TensorP, [_vp, TensorP]),
+    "gptc_gelu_forward_bias": (TensorP, [_vp, TensorP, TensorP]),
+    "gptc_gelu_backward_bias": (TensorP, [_vp, TensorP, TensorP, TensorP]),
+    "gptc_gelu_forward_bias_cuda": (None, [TensorP, TensorP, TensorP]),
+    "gptc_gelu_backward_bias_cuda": (None, [TensorP, TensorP, TensorP, TensorP, TensorP]),
     "gptc_attention_forward_qkv_bias": (None, [TensorP, TensorP, TensorP, _ci, ctypes.POINTER(TensorP), TensorP]),
     "gptc_attention_backward_qkv_bias": (None, [TensorP, ctypes.POINTER(TensorP), TensorP, _ci, TensorP, TensorP]),
     "gptc_attention_block_schedule": (_ci, [_ci, _ci, _ci, _ci, ctypes.POINTER(_ci), ctypes.POINTER(_ci), _ci,

@@ -34,6 +34,17 @@ typedef struct softmax {
 gelu_t *GELU(void);
 softmax_t *Softmax(void);
 
+/* No counterpart in the reference: GELU of x + bias (bias per last-dim
+ * column), for the library's MLP, whose c_fc Linear then runs without its
+ * bias (gptc_linear_forward_nobias): one pass over the activations instead
+ * of gpt.c's bias add followed by GELU (src/mlp.c's forward).  forward
+ * caches x (without the bias) as forward does; backward returns
+ * dx = g * gelu'(x + bias), adds its column sums to db (c_fc's bias
+ * gradient, which gptc_linear_backward_nodb then leaves alone) and consumes
+ * g and the cache. */
+tensor_t *gptc_gelu_forward_bias(gelu_t *gelu, tensor_t *x, const tensor_t *bias);
+tensor_t *gptc_gelu_backward_bias(gelu_t *gelu, tensor_t *global_grad, const tensor_t *bias, tensor_t *db);
+
 #ifdef __cplusplus
 }
 #endif

@@ -122,6 +122,23 @@ void gptc_attention_backward_qkv_bias(const tensor_t *global_grad, tensor_t **ca
                                       const int n_heads, tensor_t *dout, tensor_t *db);
 
 /*
+ * gptc_gelu_forward_bias_cuda(input, bias, output)
+ *   output = gelu(input + bias), bias per last-dim column.  No counterpart in
+ *   the reference, whose MLP adds c_fc's bias in the Linear and then runs
+ *   GELU (src/mlp.c): here the MLP's c_fc runs without it and this adds it
+ *   on the way into GELU (one pass over the 8192 x 3072 activations at
+ *   GPT-2 small's B=8 T=1024 instead of two).
+ * gptc_gelu_backward_bias_cuda(global_grad, cache, bias, dout, db)
+ *   dout = global_grad * gelu'(cache + bias) (written), and db += the column
+ *   sums of dout, formed from per-workgroup partials as dout is written and
+ *   added in a fixed order (deterministic): c_fc's bias gradient without a
+ *   second pass over dout.
+ */
+void gptc_gelu_forward_bias_cuda(const tensor_t *input, const tensor_t *bias, tensor_t *output);
+void gptc_gelu_backward_bias_cuda(const tensor_t *global_grad, const tensor_t *cache, const tensor_t *bias,
+                                  tensor_t *dout, tensor_t *db);
+
+/*
  * gptc_layer_norm_backward_set(global_grad, cache, W, dW, db, dout)
  *   As layer_norm_backward_cuda_kernel, but dout = dx instead of dout += dx
  *   (dout is not read).  No counterpart in the reference: gpt.c's LayerNorm

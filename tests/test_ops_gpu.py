@@ -154,6 +154,50 @@ def test_gelu(dev, ops, n):
     check("gelu'", dev.get(dx), ops.gelu_backward(g, x))
 
 
+def test_gelu_extreme_inputs(dev, ops):
+    """Saturated inputs give exactly x and 0 (and slopes 1 and 0), tiny ones
+    the linear part, NaN stays NaN; errors stay within the elementwise
+    tolerance over [-30, 30]."""
+    x = np.concatenate([np.linspace(-30, 30, 6001), [-1e30, -100.0, 100.0, 1e30], np.logspace(-30, -1, 31),
+                        -np.logspace(-30, -1, 31), [0.0, -0.0]]).astype(np.float32)
+    g = np.ones_like(x)
+    y, dx = dev.empty(x.shape), dev.empty(x.shape)
+    xt = dev(x)
+    dev.rt.lib.gelu_forward_cuda_kernel(xt, y)
+    dev.rt.lib.gelu_backward_cuda_kernel(dev(g), xt, dx)
+    yg, dg = dev.get(y), dev.get(dx)
+    ok = np.abs(x) < 1e29  # x**3 overflows past about 1e12 (both sides give inf * 0 or saturate)
+    check("gelu (wide range)", yg[ok], ops.gelu_forward(x)[ok])
+    check("gelu' (wide range)", dg[ok], ops.gelu_backward(g, x)[ok])
+    big = (np.abs(x) >= 10) & ok
+    assert np.array_equal(yg[big & (x > 0)], x[big & (x > 0)]) and np.all(yg[big & (x < 0)] == 0)
+    assert np.all(dg[big & (x > 0)] == 1) and np.all(dg[big & (x < 0)] == 0)
+    xn = dev(np.array([np.nan, 1.0], np.float32))
+    yn = dev.empty((2,))
+    dev.rt.lib.gelu_forward_cuda_kernel(xn, yn)
+    assert np.isnan(dev.get(yn)[0])
+
+
+@pytest.mark.parametrize("B,T,C", [(8, 33, 3072), (2, 5, 7), (1, 1, 4), (3, 100, 768)])
+def test_gelu_with_bias(dev, ops, B, T, C):
+    """The MLP's fused form: gelu(x + b) forward; backward dx = g gelu'(x + b)
+    and db += the column sums of dx (float4 path for C % 4 == 0, the scalar
+    path plus the column-sum kernels otherwise)."""
+    print(f"case gelu+bias B={B} T={T} C={C}")
+    x, b, g = rnd(B, T, C, scale=2.0), rnd(C), rnd(B, T, C)
+    db0 = rnd(C)
+    y, dx = dev.empty((B, T, C)), dev.empty((B, T, C))
+    xt, bt, db_t = dev(x), dev(b), dev(db0)
+    dev.rt.lib.gptc_gelu_forward_bias_cuda(xt, bt, y)
+    xb = (x + b).astype(np.float32)
+    check("gelu(x + b)", dev.get(y), ops.gelu_forward(xb))
+    dev.rt.lib.gptc_gelu_backward_bias_cuda(dev(g), xt, bt, dx, db_t)
+    dx_ref = ops.gelu_backward(g, xb)
+    check("dx", dev.get(dx), dx_ref)
+    db_ref = db0.astype(np.float64) + dx_ref.astype(np.float64).reshape(-1, C).sum(0)
+    check("db (accumulated)", dev.get(db_t), db_ref, atol=1e-5 * max(1, B * T) ** 0.5)
+
+
 @pytest.mark.parametrize("rows,C", [(15, 37), (8, 50257), (3, 1), (700, 64)])
 def test_softmax(dev, ops, rows, C):
     x, g = rnd(rows, C, scale=3.0), rnd(rows, C)
