@@ -8,9 +8,18 @@
 // C (M x N) = op(A) op(B) is the column-major C^T (N x M) = op(B)^T op(A)^T,
 // so each call swaps the operands and the M/N sizes and keeps the leading
 // dimensions, as the reference does for cuBLAS.
+// rocblas_gemm_ex's solution_index is part of the stable API; only the
+// listing of solutions (used by the tuner, not here) is a beta feature.
 #include <rocblas/rocblas.h>
+#include <atomic>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <set>
+#include <tuple>
 #include "blas.hpp"
+#include "gemm_tuned.hpp"
 #include "gpu_kernels.h"
 #include "hip_check.hpp"
 #include "utils.h"
@@ -98,12 +107,127 @@ void gptc_blas_destroy() {
     g_handle_stream = nullptr;
 }
 
+namespace {
+
+// Tuned solutions.  rocBLAS picks a Tensile kernel for a GEMM by a heuristic;
+// for the GEMMs of a GPT-2 small training step that pick runs 5-24 % slower
+// than the fastest solution rocBLAS itself lists for the same problem.  The
+// table gemm_tuned.inc (written by tune_gemm from a log of the library's own
+// calls, see gemm_tuned.hpp) names that solution per problem.  A listed
+// problem is run with its solution, checked by rocBLAS on first use; a
+// solution that this rocBLAS rejects (another version) is dropped with one
+// warning and the problem runs on the default pick, as every unlisted one
+// does.  The choice is fixed per problem, so results stay deterministic.
+const gptc::GemmTuned kTuned[] = {
+    {{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0},  // never matches: GEMMs with m = 0 return before the lookup
+#include "gemm_tuned.inc"
+};
+constexpr int kNumTuned = sizeof(kTuned) / sizeof(kTuned[0]);
+std::atomic<signed char> g_tuned_state[kNumTuned > 0 ? kNumTuned : 1];  // 0 untried, 1 accepted, -1 rejected
+
+int find_tuned(const gptc::GemmProblem &p) {
+    for (int i = 0; i < kNumTuned; ++i)
+        if (kTuned[i].problem == p) return i;
+    return -1;
+}
+
+// GPTC_GEMM_LOG=path: append each distinct problem this process runs to
+// path, one line each (the tuner's input).
+void log_problem(const gptc::GemmProblem &p) {
+    static const char *path = std::getenv("GPTC_GEMM_LOG");
+    if (path == nullptr || *path == '\0') return;
+    static std::mutex mu;
+    static std::set<std::tuple<int, int, int, int, int, int, int, int, long long, long long, long long, int, int, int>>
+        seen;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!seen.insert(std::make_tuple(p.ta, p.tb, p.m, p.n, p.k, p.lda, p.ldb, p.ldc, p.sa, p.sb, p.sc, p.batch,
+                                     p.beta_zero, p.alpha_one))
+             .second)
+        return;
+    FILE *f = std::fopen(path, "a");
+    if (f == nullptr) return;
+    std::fprintf(f, "%d %d %d %d %d %d %d %d %lld %lld %lld %d %d %d\n", p.ta, p.tb, p.m, p.n, p.k, p.lda, p.ldb, p.ldc,
+                 p.sa, p.sb, p.sc, p.batch, p.beta_zero, p.alpha_one);
+    std::fclose(f);
+}
+
+// rocblas_gemm_ex / _strided_batched_ex of p with solution sol and flags.
+rocblas_status gemm_ex(const gptc::GemmProblem &p, int sol, uint32_t flags, float alpha, const float *A,
+                       const float *B, float beta, float *C) {
+    const rocblas_operation ta = p.ta ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_operation tb = p.tb ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_datatype f32 = rocblas_datatype_f32_r;
+    if (p.batch == 0)
+        return rocblas_gemm_ex(gptc_blas_handle(), ta, tb, p.m, p.n, p.k, &alpha, A, f32, p.lda, B, f32, p.ldb, &beta,
+                               C, f32, p.ldc, C, f32, p.ldc, f32, rocblas_gemm_algo_solution_index, sol, flags);
+    return rocblas_gemm_strided_batched_ex(gptc_blas_handle(), ta, tb, p.m, p.n, p.k, &alpha, A, f32, p.lda, p.sa, B,
+                                           f32, p.ldb, p.sb, &beta, C, f32, p.ldc, p.sc, C, f32, p.ldc, p.sc, p.batch,
+                                           f32, rocblas_gemm_algo_solution_index, sol, flags);
+}
+
+// The tuned solution of p, run; false when p has none (or it was rejected).
+// On first use the solution is validated (rocblas_gemm_flags_check_solution_index
+// only checks the index; it does not compute), then every call runs it.
+bool run_tuned(const gptc::GemmProblem &p, float alpha, const float *A, const float *B, float beta, float *C) {
+    const int i = find_tuned(p);
+    if (i < 0) return false;
+    const signed char state = g_tuned_state[i].load(std::memory_order_relaxed);
+    if (state < 0) return false;
+    if (state == 0) {
+        const rocblas_status st =
+            gemm_ex(p, kTuned[i].solution, rocblas_gemm_flags_check_solution_index, alpha, A, B, beta, C);
+        if (st != rocblas_status_success) {
+            g_tuned_state[i].store(-1, std::memory_order_relaxed);
+            std::fprintf(stderr,
+                         "gptc: rocBLAS rejects tuned solution %d for a %dx%dx%d GEMM (%s); using its default pick.\n",
+                         kTuned[i].solution, p.m, p.n, p.k, rocblas_status_to_string(st));
+            return false;
+        }
+        g_tuned_state[i].store(1, std::memory_order_relaxed);
+    }
+    blas_check(gemm_ex(p, kTuned[i].solution, rocblas_gemm_flags_none, alpha, A, B, beta, C),
+               "gemm_ex (tuned solution)");
+    return true;
+}
+
+gptc::GemmProblem problem(rocblas_operation ta, rocblas_operation tb, int m, int n, int k, int lda, int ldb, int ldc,
+                          long long sa, long long sb, long long sc, int batch, float alpha, float beta) {
+    gptc::GemmProblem p;
+    p.ta = ta == rocblas_operation_transpose;
+    p.tb = tb == rocblas_operation_transpose;
+    p.m = m, p.n = n, p.k = k, p.lda = lda, p.ldb = ldb, p.ldc = ldc;
+    p.sa = sa, p.sb = sb, p.sc = sc, p.batch = batch;
+    p.beta_zero = beta == 0.0f;
+    p.alpha_one = alpha == 1.0f;
+    return p;
+}
+
+// Column-major rocBLAS GEMM / strided-batched GEMM, through the tuned table.
+void colmajor_gemm(rocblas_operation ta, rocblas_operation tb, int m, int n, int k, float alpha, const float *A,
+                   int lda, const float *B, int ldb, float beta, float *C, int ldc, const char *what) {
+    const gptc::GemmProblem p = problem(ta, tb, m, n, k, lda, ldb, ldc, 0, 0, 0, 0, alpha, beta);
+    log_problem(p);
+    if (run_tuned(p, alpha, A, B, beta, C)) return;
+    blas_check(rocblas_sgemm(gptc_blas_handle(), ta, tb, m, n, k, &alpha, A, lda, B, ldb, &beta, C, ldc), what);
+}
+
+void colmajor_gemm_batched(rocblas_operation ta, rocblas_operation tb, int m, int n, int k, float alpha,
+                           const float *A, int lda, long long sa, const float *B, int ldb, long long sb, float beta,
+                           float *C, int ldc, long long sc, int batch, const char *what) {
+    const gptc::GemmProblem p = problem(ta, tb, m, n, k, lda, ldb, ldc, sa, sb, sc, batch, alpha, beta);
+    log_problem(p);
+    if (run_tuned(p, alpha, A, B, beta, C)) return;
+    blas_check(rocblas_sgemm_strided_batched(gptc_blas_handle(), ta, tb, m, n, k, &alpha, A, lda, sa, B, ldb, sb,
+                                             &beta, C, ldc, sc, batch),
+               what);
+}
+
+}  // namespace
+
 void gptc_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float *A, int lda, const float *B,
                 int ldb, float beta, float *C, int ldc) {
     if (M <= 0 || N <= 0) return;
-    blas_check(rocblas_sgemm(gptc_blas_handle(), op(trans_b), op(trans_a), N, M, K, &alpha, B, ldb, A, lda, &beta, C,
-                             ldc),
-               "sgemm");
+    colmajor_gemm(op(trans_b), op(trans_a), N, M, K, alpha, B, ldb, A, lda, beta, C, ldc, "sgemm");
 }
 
 namespace {
@@ -163,11 +287,9 @@ void gptc_sgemm_wgrad(int out_f, int in_f, int rows, const float *g, const float
     float *partial = static_cast<float *>(alloc_cuda(sizeof(float) * static_cast<size_t>(n) * S));
     const float one = 1.0f, zero = 0.0f;
     // Column-major view: partial_b^T (in x out) = x_b^T (in x chunk) g_b (chunk x out).
-    blas_check(rocblas_sgemm_strided_batched(gptc_blas_handle(), rocblas_operation_none, rocblas_operation_transpose,
-                                             in_f, out_f, chunk, &one, x, in_f,
-                                             static_cast<rocblas_stride>(chunk) * in_f, g, out_f,
-                                             static_cast<rocblas_stride>(chunk) * out_f, &zero, partial, in_f, n, S),
-               "sgemm_strided_batched (weight gradient)");
+    colmajor_gemm_batched(rocblas_operation_none, rocblas_operation_transpose, in_f, out_f, chunk, one, x, in_f,
+                          static_cast<long long>(chunk) * in_f, g, out_f, static_cast<long long>(chunk) * out_f, zero,
+                          partial, in_f, n, S, "sgemm_strided_batched (weight gradient)");
     launch_add_partials(partial, dW, n, S, true, s);
     free_cuda(partial);
 }
@@ -195,15 +317,13 @@ void gptc_sgemm_dgrad(int rows, int in_f, int out_f, const float *g, const float
     const float one = 1.0f, zero = 0.0f;
     // Column-major view: partial_b^T (in x rows) = W_b^T (in x chunk) g_b^T (chunk x rows),
     // W_b = rows [b*chunk, (b+1)*chunk) of W, g_b = the same columns of g.
-    blas_check(rocblas_sgemm_strided_batched(gptc_blas_handle(), rocblas_operation_none, rocblas_operation_none, in_f,
-                                             rows, chunk, &one, W, in_f, static_cast<rocblas_stride>(chunk) * in_f, g,
-                                             out_f, chunk, &zero, partial, in_f, n, S),
-               "sgemm_strided_batched (input gradient)");
+    colmajor_gemm_batched(rocblas_operation_none, rocblas_operation_none, in_f, rows, chunk, one, W, in_f,
+                          static_cast<long long>(chunk) * in_f, g, out_f, chunk, zero, partial, in_f, n, S,
+                          "sgemm_strided_batched (input gradient)");
     if (rest > 0) {
         const int64_t k0 = static_cast<int64_t>(S) * chunk;
-        blas_check(rocblas_sgemm(gptc_blas_handle(), rocblas_operation_none, rocblas_operation_none, in_f, rows, rest,
-                                 &one, W + k0 * in_f, in_f, g + k0, out_f, &one, partial, in_f),
-                   "sgemm (input gradient, leftover terms)");
+        colmajor_gemm(rocblas_operation_none, rocblas_operation_none, in_f, rows, rest, one, W + k0 * in_f, in_f,
+                      g + k0, out_f, one, partial, in_f, "sgemm (input gradient, leftover terms)");
     }
     launch_add_partials(partial, dx, n, S, false, s);
     free_cuda(partial);
@@ -231,9 +351,8 @@ extern "C" void sgemm_strided_batched_cuda(const int TransA, const int TransB, c
     check_matrix(A, nb * strideA, TransA == 1 ? K : M, TransA == 1 ? M : K, lda, "sgemm_strided_batched A");
     check_matrix(B, nb * strideB, TransB == 1 ? N : K, TransB == 1 ? K : N, ldb, "sgemm_strided_batched B");
     check_matrix(C, nb * strideC, M, N, ldc, "sgemm_strided_batched C");
-    blas_check(rocblas_sgemm_strided_batched(gptc_blas_handle(), op(TransB), op(TransA), N, M, K, &alpha, B->t, ldb,
-                                             strideB, A->t, lda, strideA, &beta, C->t, ldc, strideC, batch_count),
-               "sgemm_strided_batched");
+    colmajor_gemm_batched(op(TransB), op(TransA), N, M, K, alpha, B->t, ldb, strideB, A->t, lda, strideA, beta, C->t,
+                          ldc, strideC, batch_count, "sgemm_strided_batched");
 }
 
 extern "C" void saxpy_cuda(const int n, const float alpha, const tensor_t *x, const int offsetx, const int incx,

@@ -105,6 +105,31 @@ def test_linear(dev, ops, B, T, in_f, out_f, bias):
         check("db (accumulated)", dev.get(db_t), db, rtol=2e-5)
 
 
+@pytest.mark.parametrize("in_f,out_f", [(768, 3072), (3072, 768), (768, 2304)])
+def test_linear_tuned_gemm_shapes(dev, in_f, out_f):
+    """GPT-2's Linear shapes at C3's 8192 rows run rocBLAS solutions from
+    the library's tuned table (csrc/gemm_tuned.inc).  Outputs prefilled with
+    NaN: a solution's first call (validated, then run) must compute every
+    entry and read nothing of C where beta = 0.  Checked against float64
+    numpy: y and dx on every 61st row, dW in full (accumulated onto dW0)."""
+    print(f"case tuned linear in={in_f} out={out_f}")
+    B, T = 8, 1024
+    x, W, g = rnd(B, T, in_f), rnd(out_f, in_f, scale=0.02), rnd(B, T, out_f)
+    b, dW0, db0 = rnd(out_f), rnd(out_f, in_f), rnd(out_f)
+    y = dev(np.full((B, T, out_f), np.nan, np.float32))
+    dev.rt.lib.linear_forward_cuda_kernel(dev(W), dev(b), dev(x), y)
+    x2, g2 = x.reshape(-1, in_f).astype(np.float64), g.reshape(-1, out_f).astype(np.float64)
+    W64 = W.astype(np.float64)
+    y_ref = x2[::61] @ W64.T + b
+    check("y (every 61st row)", dev.get(y).reshape(-1, out_f)[::61], y_ref, rtol=2e-5)
+    dW_t, db_t = dev(dW0), dev(db0)
+    dx = dev(np.full((B, T, in_f), np.nan, np.float32))
+    dev.rt.lib.linear_backward_cuda_kernel(dev(g), dev(x), dev(W), dW_t, db_t, dx)
+    check("dx (every 61st row)", dev.get(dx).reshape(-1, in_f)[::61], g2[::61] @ W64, rtol=2e-5)
+    check("dW (accumulated)", dev.get(dW_t), dW0 + g2.T @ x2, rtol=2e-5)
+    check("db (accumulated)", dev.get(db_t), db0 + g2.sum(0), rtol=2e-5)
+
+
 @pytest.mark.parametrize("B,T,C", [(2, 7, 48), (4, 64, 768), (3, 5, 1600), (1, 3, 2048), (2, 3, 5), (8, 33, 1024)])
 def test_layer_norm(dev, ops, B, T, C):
     print(f"case layer_norm B={B} T={T} C={C}")
