@@ -271,12 +271,31 @@ void launch_add_partials(const float *partial, float *out, int64_t n, int S, boo
 
 void gptc_sgemm_wgrad(int out_f, int in_f, int rows, const float *g, const float *x, float *dW) {
     if (out_f <= 0 || in_f <= 0) return;
-    // Output tiles of 128 x 128; below about two per CU the GEMM cannot fill
-    // 256 CUs, so the row (K) range is split into S slices computed as one
-    // strided-batched GEMM, and the slices are added in a fixed order.
-    const int64_t tiles = static_cast<int64_t>((out_f + 127) / 128) * ((in_f + 127) / 128);
-    int S = 1;
-    while (S < 8 && tiles * S < 512 && rows % (2 * S) == 0 && rows / (2 * S) >= 1024) S *= 2;
+    // Output tiles of 128 x 128; below about two per CU rocBLAS's default
+    // pick cannot fill 256 CUs, so the row (K) range is split into S slices
+    // computed as one strided-batched GEMM, and the slices are added in a
+    // fixed order.
+    // A tuned solution for one of the split counts 1, 2, 4, 8 fixes S: the
+    // table holds one per weight gradient, chosen with the slices' add pass
+    // counted (with tuned kernels GPT-2's c_fc and c_proj products fill the
+    // GPU unsplit).
+    const int64_t n_out = static_cast<int64_t>(out_f) * in_f;
+    int S = 0;
+    for (int s = 1; s <= 8 && S == 0; s *= 2) {
+        if (rows % s != 0) continue;
+        const int c = rows / s;
+        const gptc::GemmProblem p =
+            s == 1 ? problem(rocblas_operation_none, rocblas_operation_transpose, in_f, out_f, rows, in_f, out_f, in_f,
+                             0, 0, 0, 0, 1.0f, 1.0f)
+                   : problem(rocblas_operation_none, rocblas_operation_transpose, in_f, out_f, c, in_f, out_f, in_f,
+                             static_cast<long long>(c) * in_f, static_cast<long long>(c) * out_f, n_out, s, 1.0f, 0.0f);
+        if (find_tuned(p) >= 0) S = s;
+    }
+    if (S == 0) {
+        const int64_t tiles = static_cast<int64_t>((out_f + 127) / 128) * ((in_f + 127) / 128);
+        S = 1;
+        while (S < 8 && tiles * S < 512 && rows % (2 * S) == 0 && rows / (2 * S) >= 1024) S *= 2;
+    }
     if (S == 1) {
         gptc_sgemm(1, 0, out_f, in_f, rows, 1.0f, g, out_f, x, in_f, 1.0f, dW, in_f);
         return;

@@ -12,6 +12,12 @@
 // default's result to 1e-5 of its largest entry and gives identical bits on
 // a repeat.  Solution indices are those of this image's rocBLAS; another
 // rocBLAS rejects them on first use and the default pick runs instead.
+//
+// Weight gradients: gptc_sgemm_wgrad uses the split count S of a tuned entry
+// when the table has one for its product at S = 1, 2, 4 or 8 (one per
+// product), else its tile-count rule.  Those entries come from a tune_gemm
+// run over the four split counts of each product (log lines written by hand
+// in the format above), the fastest GEMM plus its slices' add pass chosen.
 #pragma once
 
 namespace gptc {
