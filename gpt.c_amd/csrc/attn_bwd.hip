@@ -52,60 +52,37 @@ constexpr int kBwdBQ = 64;   // queries per LDS tile in the dk/dv kernel
 constexpr int kBwdBM = 128;  // queries per dq workgroup (32 per wave)
 constexpr int kBwdBN = 64;   // keys per LDS tile in the dq kernel
 
-// ---- delta = rowsum(dO o O): 16 lanes per (b, t, h) row, 64 rows per workgroup ----
-// A 16-lane group takes kDeltaRows rows 16 apart (each step of the workgroup
-// covers 16 consecutive rows of memory) and issues the loads of all of them
-// before the first sum.
-constexpr int kDeltaRows = 4;
-
+// ---- delta = rowsum(dO o O): 16 lanes per (b, t, h) row, 16 rows per workgroup ----
 template <bool VEC>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams a) {
     const int l16 = threadIdx.x & 15;
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4);  // (b*T + t)*H + h: memory order of (B, T, C)
     const int rows = a.B * a.T * a.H;
-    const int row0 = blockIdx.x * (16 * kDeltaRows) + (threadIdx.x >> 4);  // (b*T + t)*H + h: memory order of (B, T, C)
-    const float *op[kDeltaRows], *gp[kDeltaRows];
-    int bb[kDeltaRows], tt[kDeltaRows], hh[kDeltaRows];
-    float sum[kDeltaRows];
-#pragma unroll
-    for (int u = 0; u < kDeltaRows; ++u) {
-        const int row = min(row0 + 16 * u, rows - 1);  // a row past the end repeats the last one, not stored
-        hh[u] = row % a.H;
+    float sum = 0.0f;
+    int b = 0, t = 0, h = 0;
+    if (row < rows) {
+        h = row % a.H;
         const int bt = row / a.H;
-        tt[u] = bt % a.T;
-        bb[u] = bt / a.T;
-        op[u] = a.o.p + bb[u] * a.o.sb + tt[u] * a.o.st + hh[u] * a.o.sh;
-        gp[u] = a.dout.p + bb[u] * a.dout.sb + tt[u] * a.dout.st + hh[u] * a.dout.sh;
-        sum[u] = 0.0f;
-    }
-    if (VEC) {
-        for (int d = 4 * l16; d < a.D; d += 64) {
-            f32x4 x[kDeltaRows], y[kDeltaRows];
-#pragma unroll
-            for (int u = 0; u < kDeltaRows; ++u) {
-                x[u] = load4<true>(op[u], d, a.D);
-                y[u] = load4<true>(gp[u], d, a.D);
+        t = bt % a.T;
+        b = bt / a.T;
+        const float *o = a.o.p + b * a.o.sb + t * a.o.st + h * a.o.sh;
+        const float *g = a.dout.p + b * a.dout.sb + t * a.dout.st + h * a.dout.sh;
+        if (VEC) {
+            for (int d = 4 * l16; d < a.D; d += 64) {
+                const f32x4 x = load4<true>(o, d, a.D), y = load4<true>(g, d, a.D);
+                sum += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
             }
-#pragma unroll
-            for (int u = 0; u < kDeltaRows; ++u)
-                sum[u] += x[u][0] * y[u][0] + x[u][1] * y[u][1] + x[u][2] * y[u][2] + x[u][3] * y[u][3];
+        } else {
+            for (int d = l16; d < a.D; d += 16) sum = fmaf(o[d], g[d], sum);
         }
-    } else {
-#pragma unroll
-        for (int u = 0; u < kDeltaRows; ++u)
-            for (int d = l16; d < a.D; d += 16) sum[u] = fmaf(op[u][d], gp[u][d], sum[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kDeltaRows; ++u) {
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) sum[u] += __shfl_xor(sum[u], off, 16);
-        if (row0 + 16 * u >= rows) continue;
-        const uint32_t b = bb[u], t = tt[u], h = hh[u];
-        if (l16 == 0) a.delta[(b * a.H + h) * a.T + t] = sum[u];
-        // dK, dV rows of the split key blocks start at zero (D == 64, 16-byte rows).
-        if (VEC && static_cast<int>(t) < a.nsplit * kBwdBK) {
-            *reinterpret_cast<f32x4 *>(a.dk.p + b * a.dk.sb + t * a.dk.st + h * a.dk.sh + 4 * l16) = zero4();
-            *reinterpret_cast<f32x4 *>(a.dv.p + b * a.dv.sb + t * a.dv.st + h * a.dv.sh + 4 * l16) = zero4();
-        }
+    for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+    if (row < rows && l16 == 0) a.delta[(static_cast<uint32_t>(b) * a.H + h) * a.T + t] = sum;
+    // dK, dV rows of the split key blocks start at zero (D == 64, 16-byte rows).
+    if (VEC && row < rows && t < a.nsplit * kBwdBK) {
+        *reinterpret_cast<f32x4 *>(a.dk.p + b * a.dk.sb + t * a.dk.st + h * a.dk.sh + 4 * l16) = zero4();
+        *reinterpret_cast<f32x4 *>(a.dv.p + b * a.dv.sb + t * a.dv.st + h * a.dv.sh + 4 * l16) = zero4();
     }
 }
 
@@ -1363,7 +1340,7 @@ void launch_attn_bwd(const BwdParams &p_in, hipStream_t stream, const hipEvent_t
     }
     const dim3 block(256);
     const int rows = p.B * p.T * p.H;
-    const dim3 grid_d((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows)), grid_k(p.nkb * p.bh_pad), grid_q(p.nqb * p.bh_pad);
+    const dim3 grid_d((rows + 15) / 16), grid_k(p.nkb * p.bh_pad), grid_q(p.nqb * p.bh_pad);
     if (ev) hipCheck(hipEventRecord(ev[0], stream));
     if (p.vec)
         attn_bwd_delta_kernel<true><<<grid_d, block, 0, stream>>>(p);
