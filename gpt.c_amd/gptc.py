@@ -238,8 +238,8 @@ MT19937_STATE_BYTES = 8 + 4 + 4 + 624 * 4 + 2 * 4  # mt19937_state in include/ra
 
 
 def build():
-    """Compile libgptc_amd.so for gfx950 (hipcc + gcc; cross-compiles without a GPU)."""
-    subprocess.run(["make", "-B", "-j8", "-C", HERE], check=True, stdout=subprocess.DEVNULL)
+    """Compile libgptc_amd.so for gfx950 (hipcc + gcc; cross-compiles without a GPU), and the GEMM tuner."""
+    subprocess.run(["make", "-B", "-j8", "-C", HERE, "all", "tune"], check=True, stdout=subprocess.DEVNULL)
 
 
 def load(path=None):
