@@ -92,6 +92,39 @@ __global__ __launch_bounds__(kThreads) void gelu_bias_fwd_kernel(const float *__
     for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) y[i] = gelu_f(h[i] + b[static_cast<uint32_t>(i) % static_cast<uint32_t>(cols)]);
 }
 
+// The same on float4 columns with a fixed column per thread: workgroup
+// (x, y) covers float4 columns [256 x, 256 x + 256) of rows y, y + gridDim.y,
+// ..., four rows per round with their loads issued together; the bias is
+// loaded once per thread and no index is divided.
+__global__ __launch_bounds__(kThreads) void gelu_bias_fwd4_kernel(const float *__restrict__ h,
+                                                                 const float *__restrict__ b, float *__restrict__ y,
+                                                                 int rows, int c4n) {
+    const int c4 = blockIdx.x * kThreads + threadIdx.x;
+    if (c4 >= c4n) return;
+    const f32x4_t *h4 = reinterpret_cast<const f32x4_t *>(h);
+    f32x4_t *y4 = reinterpret_cast<f32x4_t *>(y);
+    const f32x4_t bv = reinterpret_cast<const f32x4_t *>(b)[c4];
+    const int ry = gridDim.y;
+    for (int r0 = blockIdx.y; r0 < rows; r0 += 4 * ry) {
+        f32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = min(r0 + u * ry, rows - 1);  // past the end: repeats a row, not stored
+            v[u] = h4[static_cast<int64_t>(r) * c4n + c4];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = r0 + u * ry;
+            if (r < rows) {
+                f32x4_t o = v[u] + bv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = gelu_f(o[e]);
+                y4[static_cast<int64_t>(r) * c4n + c4] = o;
+            }
+        }
+    }
+}
+
 // dout = g * gelu'(h + b[c]) over rows x cols (float4 columns, 16-byte
 // aligned), and partial[blockIdx.y, c] = the column sums of dout over rows
 // r0 .. r0 + rpp - 1 of part blockIdx.y (the bias gradient's partials, added
@@ -257,9 +290,18 @@ extern "C" void gptc_gelu_forward_bias_cuda(const tensor_t *input, const tensor_
     CHECK_ERROR(output->length != input->length, "Expected output to match input's %d elements.", input->length);
     if (rows == 0 || cols == 0) return;
     const bool vec = cols % 4 == 0 && aligned16(input->t) && aligned16(bias->t) && aligned16(output->t);
-    const int64_t items = static_cast<int64_t>(rows) * (vec ? cols / 4 : cols);
-    gelu_bias_fwd_kernel<<<dim3(blocks_for(items, kThreads)), dim3(kThreads), 0, gptc_stream_checked()>>>(
-        input->t, bias->t, output->t, rows, cols, vec);
+    if (vec) {
+        // About 2048 workgroups: the column blocks times row strides.
+        const int cblocks = (cols / 4 + kThreads - 1) / kThreads;
+        int ry = (2048 + cblocks - 1) / cblocks;
+        if (ry > rows) ry = rows;
+        if (ry > 65535) ry = 65535;
+        gelu_bias_fwd4_kernel<<<dim3(cblocks, ry), dim3(kThreads), 0, gptc_stream_checked()>>>(
+            input->t, bias->t, output->t, rows, cols / 4);
+    } else {
+        gelu_bias_fwd_kernel<<<dim3(blocks_for(static_cast<int64_t>(rows) * cols, kThreads)), dim3(kThreads), 0,
+                               gptc_stream_checked()>>>(input->t, bias->t, output->t, rows, cols, false);
+    }
     hipCheck(hipGetLastError());
 }
 

@@ -4,15 +4,16 @@
 //   forward   cache[0] = log_softmax(logits) per row; output[0] = mean over
 //             rows of -log_softmax[target];
 //   backward  with s = -g / (B T):  dout[j] = [j == target] s - exp(lsm[j]) s.
-// A row is one workgroup.  Rows of up to 65536 logits (16-byte aligned
-// buffers) are held in the registers of a 512-thread workgroup: one read of
-// the logits, then the max, the sum and the log-softmax from registers.
-// Longer rows take one online (max, sum) pass over the logits, then a pass
-// that writes the log-softmax (float4 accesses and exp2 where aligned).
-// The per-row losses go to a buffer and one workgroup adds them in a fixed
-// order, so the mean is deterministic.  A target outside [0, V) makes that row's loss NaN (the
-// reference would read outside the row) and its gradient row is the softmax
-// part only.
+// Forward: a row is one workgroup.  Rows of up to 65536 logits (16-byte
+// aligned buffers) are held in the registers of a 512-thread workgroup: one
+// read of the logits, then the max, the sum and the log-softmax from
+// registers.  Longer rows take one online (max, sum) pass over the logits,
+// then a pass that writes the log-softmax (float4 accesses and exp2 where
+// aligned).  The per-row losses go to a buffer and one workgroup adds them
+// in a fixed order, so the mean is deterministic.  Backward: elementwise,
+// several workgroups per row.  A target outside [0, V) makes that row's loss
+// NaN (the reference would read outside the row) and its gradient row is the
+// softmax part only.
 #include "gpu_kernels.h"
 #include "ops_common.hpp"
 
@@ -197,12 +198,11 @@ __global__ __launch_bounds__(kThreads) void ce_bwd4_kernel(const float *__restri
     if (je >= 0) dr[je] = (je == t ? s : 0.0f) - __builtin_amdgcn_exp2f(lr[je] * kLog2eF) * s;
 }
 
-// Row-resident forms of the two kernels for rows of at most 512 NPT float4
-// (GPT-2's V = 50257 takes NPT = 25): a 512-thread workgroup issues every
-// load of its row before the first use and keeps the row in registers, so
-// the forward reads the logits once (max, then the sum of exponentials, then
-// the output, all from registers; 8 V bytes per row instead of 12 V) and
-// the backward's loads are not held behind its stores.
+// Row-resident forward for rows of at most 512 NPT float4 (GPT-2's
+// V = 50257 takes NPT = 25): a 512-thread workgroup issues every load of its
+// row before the first use and keeps the row in registers, so the logits are
+// read once (max, then the sum of exponentials, then the output, all from
+// registers; 8 V bytes per row instead of 12 V).
 constexpr int kRowThreads = 512;
 constexpr int kRowWaves = kRowThreads / kWave;
 
@@ -274,31 +274,37 @@ __global__ __launch_bounds__(kRowThreads) void ce_fwd_row_kernel(const float *__
     }
 }
 
-template <int NPT>
-__global__ __launch_bounds__(kRowThreads) void ce_bwd_row_kernel(const float *__restrict__ g,
-                                                                const float *__restrict__ lsm,
-                                                                const float *__restrict__ targets,
-                                                                float *__restrict__ dout, int V, float rows_f) {
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * V;
-    const float s = -g[blockIdx.x] / rows_f;
-    const int t = static_cast<int>(targets[blockIdx.x]);
+// The backward is elementwise once a row's scale s is known: a row is cut
+// into chunks of kBwdChunk float4 (4 per thread, their loads issued
+// together), one workgroup per (chunk, row); chunk 0 also takes the row's
+// unaligned ends.
+constexpr int kBwdVecs = 4;
+constexpr int kBwdChunk = kThreads * kBwdVecs;
+
+__global__ __launch_bounds__(kThreads) void ce_bwd_chunk_kernel(const float *__restrict__ g,
+                                                               const float *__restrict__ lsm,
+                                                               const float *__restrict__ targets,
+                                                               float *__restrict__ dout, int V, float rows_f) {
+    const int row = blockIdx.y;
+    const int64_t base = static_cast<int64_t>(row) * V;
+    const float s = -g[row] / rows_f;
+    const int t = static_cast<int>(targets[row]);
     int head, n4;
     row_split(base, V, head, n4);
-    const int je = row_end_index(head, head + 4 * n4, V);
     const float *lr = lsm + base;
     float *dr = dout + base;
     const f32x4_t *l4 = reinterpret_cast<const f32x4_t *>(lr + head);
     f32x4_t *d4 = reinterpret_cast<f32x4_t *>(dr + head);
-    f32x4_t l[NPT];
+    const int i0 = blockIdx.x * kBwdChunk + threadIdx.x;
+    f32x4_t l[kBwdVecs];
 #pragma unroll
-    for (int k = 0; k < NPT; ++k) {
-        const int i = threadIdx.x + k * kRowThreads;
+    for (int k = 0; k < kBwdVecs; ++k) {
+        const int i = i0 + k * kThreads;
         l[k] = i < n4 ? l4[i] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    const float le = je >= 0 ? lr[je] : 0.0f;
 #pragma unroll
-    for (int k = 0; k < NPT; ++k) {
-        const int i = threadIdx.x + k * kRowThreads;
+    for (int k = 0; k < kBwdVecs; ++k) {
+        const int i = i0 + k * kThreads;
         if (i < n4) {
             f32x4_t d;
 #pragma unroll
@@ -307,7 +313,10 @@ __global__ __launch_bounds__(kRowThreads) void ce_bwd_row_kernel(const float *__
             d4[i] = d;
         }
     }
-    if (je >= 0) dr[je] = (je == t ? s : 0.0f) - __builtin_amdgcn_exp2f(le * kLog2eF) * s;
+    if (blockIdx.x == 0) {
+        const int je = row_end_index(head, head + 4 * n4, V);
+        if (je >= 0) dr[je] = (je == t ? s : 0.0f) - __builtin_amdgcn_exp2f(lr[je] * kLog2eF) * s;
+    }
 }
 
 // NPT for a row of n4 float4 (0: too long, use the streaming kernels).
@@ -368,11 +377,10 @@ extern "C" void cross_entropy_backward_cuda_kernel(const tensor_t *global_grad, 
     CHECK_ERROR(dout->length != lsm->length, "Expected dout to match the logits' %d elements.", lsm->length);
     if (rows == 0) return;
     // The reference divides by the int B*T (cpu/CrossEntropyLoss.c:67-72).
-    const int npt = row_npt(V);
-    if (aligned16(lsm->t) && aligned16(dout->t) && npt > 0) {
-        auto k = npt == 8 ? ce_bwd_row_kernel<8> : npt == 25 ? ce_bwd_row_kernel<25> : ce_bwd_row_kernel<32>;
-        k<<<dim3(rows), dim3(kRowThreads), 0, gptc_stream_checked()>>>(global_grad->t, lsm->t, cache[1]->t, dout->t,
-                                                                       V, static_cast<float>(rows));
+    if (aligned16(lsm->t) && aligned16(dout->t) && rows <= 65535) {
+        const dim3 grid(V / 4 >= 1 ? (V / 4 + kBwdChunk - 1) / kBwdChunk : 1, rows);  // chunk 0 also takes the ends
+        ce_bwd_chunk_kernel<<<grid, dim3(kThreads), 0, gptc_stream_checked()>>>(global_grad->t, lsm->t, cache[1]->t,
+                                                                                dout->t, V, static_cast<float>(rows));
     } else if (aligned16(lsm->t) && aligned16(dout->t))
         ce_bwd4_kernel<<<dim3(rows), dim3(kThreads), 0, gptc_stream_checked()>>>(
             global_grad->t, lsm->t, cache[1]->t, dout->t, V, static_cast<float>(rows));
